@@ -1,0 +1,106 @@
+/*
+ * C-ABI of libmi355x_fp8.so: the dynamic block-scaled FP8 linear on AMD MI355X (gfx950).
+ *
+ * Contract (reference: engine/kernels/sm89_fp8.py): bf16/fp16 activations in, OCP
+ * e4m3fn weights [N, K] (K contiguous) with fp32 128x128 block scales
+ * [ceil(N/128), ceil(K/128)], bf16/fp16 out.  Activations are quantized per row and
+ * 128-wide K group: s = amax/448 (stored raw), q = e4m3fn(x / max(s, 1e-12)).  The GEMM
+ * accumulates, per 128-wide K group in increasing order, dot(q, w) * a_s * w_s in fp32.
+ *
+ * All pointers are device pointers; all sizes, strides and leading dimensions are in
+ * elements and are 64-bit.  Calls are asynchronous on `stream` (a hipStream_t, NULL =
+ * the null stream), never allocate, never synchronize, and are therefore safe to capture
+ * in a HIP graph.  Every entry point returns an MI355X_FP8_* status code.
+ */
+#ifndef MI355X_FP8_H
+#define MI355X_FP8_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MI355X_FP8_ABI_VERSION 1
+
+/* Element types of activations and outputs. */
+#define MI355X_FP8_DTYPE_BF16 0
+#define MI355X_FP8_DTYPE_F16 1
+
+/* GEMM kernel selection (the `gemm_config` of the reference's wrapper). */
+#define MI355X_FP8_CONFIG_AUTO 0
+#define MI355X_FP8_CONFIG_STREAM 1  /* weight-streaming split-K kernel, M <= 64 */
+#define MI355X_FP8_CONFIG_TILE128 2 /* LDS-tiled 128x128 MFMA kernel, any M */
+
+/* Status codes. */
+#define MI355X_FP8_OK 0
+#define MI355X_FP8_ERR_INVALID 1     /* bad size, stride or dtype (Python: ValueError) */
+#define MI355X_FP8_ERR_UNSUPPORTED 2 /* valid but not supported here (RuntimeError) */
+#define MI355X_FP8_ERR_WORKSPACE 3   /* workspace missing or too small (ValueError) */
+#define MI355X_FP8_ERR_LAUNCH 4      /* HIP launch failure (RuntimeError) */
+
+/* Version of this ABI; equals MI355X_FP8_ABI_VERSION of the header it was built with. */
+int mi355x_fp8_abi_version(void);
+
+/* Static text for a status code. */
+const char* mi355x_fp8_status_string(int status);
+
+/*
+ * Activation quantizer.  Replaces quantize_sm89_fp8_activation and its
+ * _quantize_activation_kernel (engine/kernels/sm89_fp8.py:401-424, :304-332).
+ *   x     : M x K activations of x_dtype, element (m, k) at x[m*sxm + k*sxk]
+ *   q     : e4m3fn codes, element (m, k) at q[m*ldq + k]; columns [K, kpad) are written
+ *           as code 0 (kpad >= K, kpad <= 128*ceil(K/128), ldq >= kpad)
+ *   s     : fp32 scales, element (m, g) at s[m*s_sm + g*s_sk], g < ceil(K/128)
+ * M == 0 is a no-op; K must be positive.
+ */
+int mi355x_fp8_act_quant(const void* x, int x_dtype, int64_t M, int64_t K, int64_t sxm,
+                         int64_t sxk, uint8_t* q, int64_t ldq, int64_t kpad, float* s,
+                         int64_t s_sm, int64_t s_sk, void* stream);
+
+/*
+ * Workspace bytes that mi355x_fp8_block_gemm needs for (M, N, K, config).  Every
+ * workspace begins with a fixed 256 KiB region of split-K arrival counters, so the size is
+ * never below 256 KiB.  That region must be zero-filled once when the workspace is
+ * allocated; every call leaves it zero again, so one workspace can be reused, for any
+ * shapes, by calls that are ordered on one stream.  Calls that overlap in time must not
+ * share a workspace.
+ */
+size_t mi355x_fp8_block_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int config);
+
+/*
+ * Block-scaled FP8 GEMM on pre-quantized activations.  Replaces _launch_split_gemm and
+ * _fp8_split_gemm_kernel (engine/kernels/sm89_fp8.py:427-441, :344-398).
+ *   q   : M x K e4m3fn, (m, k) at q[m*ldq + k]
+ *   as  : activation scales, (m, kb) at as[m*as_sm + kb*as_sk]
+ *   w   : N x K e4m3fn, (n, k) at w[n*ldw + k]
+ *   ws  : weight block scales, (nb, kb) at ws[nb*ws_sn + kb*ws_sk]
+ *   out : M x N of out_dtype, (m, n) at out[m*ldo + n]
+ */
+int mi355x_fp8_block_gemm(const uint8_t* q, int64_t ldq, const float* as, int64_t as_sm,
+                          int64_t as_sk, const uint8_t* w, int64_t ldw, const float* ws,
+                          int64_t ws_sn, int64_t ws_sk, void* out, int out_dtype, int64_t ldo,
+                          int64_t M, int64_t N, int64_t K, void* workspace,
+                          size_t workspace_bytes, int config, void* stream);
+
+/* Workspace bytes that mi355x_fp8_linear needs (quantized activations, their scales and
+ * the GEMM's workspace).  Same zero-once / reuse rules as the GEMM workspace. */
+size_t mi355x_fp8_linear_workspace_bytes(int64_t M, int64_t N, int64_t K, int config);
+
+/*
+ * The full linear: quantize x, then the block GEMM.  Replaces the kernel launches of
+ * sm89_fp8_linear (engine/kernels/sm89_fp8.py:488-526); the Python wrapper keeps the
+ * reference's validation, reshaping and bias handling.  Arguments as above.
+ */
+int mi355x_fp8_linear(const void* x, int x_dtype, int64_t M, int64_t K, int64_t sxm,
+                      int64_t sxk, const uint8_t* w, int64_t ldw, const float* ws,
+                      int64_t ws_sn, int64_t ws_sk, int64_t N, void* out, int out_dtype,
+                      int64_t ldo, void* workspace, size_t workspace_bytes, int config,
+                      void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MI355X_FP8_H */

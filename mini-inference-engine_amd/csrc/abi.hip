@@ -1,0 +1,116 @@
+// extern "C" entry points of libmi355x_fp8.so (declared in include/mi355x_fp8.h).
+// Argument validation lives here; the kernels assume validated shapes.
+#include "fp8_abi_internal.h"
+
+using namespace mi355x;
+
+namespace {
+
+int64_t cdiv64(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+bool valid_dtype(int d) { return d == MI355X_FP8_DTYPE_BF16 || d == MI355X_FP8_DTYPE_F16; }
+
+// Layout of the linear's workspace: [GEMM workspace | q (M x Kpad) | a_s (KB x Mpad)].
+struct LinearLayout {
+  GemmPlan plan;
+  int64_t kpad, mpad, kb;
+  size_t gemm_bytes, q_off, s_off, total;
+};
+
+int linear_layout(int64_t M, int64_t N, int64_t K, int config, LinearLayout* L) {
+  int st = plan_gemm(M, N, K, config, &L->plan);
+  if (st != MI355X_FP8_OK) return st;
+  L->kb = cdiv64(K, 128);
+  L->kpad = L->kb * 128;
+  L->mpad = cdiv64(M > 0 ? M : 1, 64) * 64;
+  L->gemm_bytes = gemm_workspace_bytes(L->plan);
+  L->q_off = align256(L->gemm_bytes);
+  L->s_off = L->q_off + align256(static_cast<size_t>(M) * static_cast<size_t>(L->kpad));
+  L->total = L->s_off + align256(static_cast<size_t>(L->kb) * static_cast<size_t>(L->mpad) * sizeof(float));
+  return MI355X_FP8_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int mi355x_fp8_abi_version(void) { return MI355X_FP8_ABI_VERSION; }
+
+const char* mi355x_fp8_status_string(int status) {
+  switch (status) {
+    case MI355X_FP8_OK: return "ok";
+    case MI355X_FP8_ERR_INVALID: return "invalid argument";
+    case MI355X_FP8_ERR_UNSUPPORTED: return "unsupported call";
+    case MI355X_FP8_ERR_WORKSPACE: return "workspace missing or too small";
+    case MI355X_FP8_ERR_LAUNCH: return "HIP kernel launch failed";
+    default: return "unknown status";
+  }
+}
+
+int mi355x_fp8_act_quant(const void* x, int x_dtype, int64_t M, int64_t K, int64_t sxm,
+                         int64_t sxk, uint8_t* q, int64_t ldq, int64_t kpad, float* s,
+                         int64_t s_sm, int64_t s_sk, void* stream) {
+  if (!valid_dtype(x_dtype) || M < 0 || K <= 0 || kpad < K || kpad > cdiv64(K, 128) * 128 || ldq < kpad)
+    return MI355X_FP8_ERR_INVALID;
+  if (M == 0) return MI355X_FP8_OK;
+  if (!x || !q || !s) return MI355X_FP8_ERR_INVALID;
+  return launch_act_quant(x, x_dtype, M, K, sxm, sxk, q, ldq, kpad, s, s_sm, s_sk,
+                          static_cast<hipStream_t>(stream));
+}
+
+size_t mi355x_fp8_block_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int config) {
+  GemmPlan plan;
+  if (plan_gemm(M, N, K, config, &plan) != MI355X_FP8_OK) return 0;
+  return gemm_workspace_bytes(plan);
+}
+
+int mi355x_fp8_block_gemm(const uint8_t* q, int64_t ldq, const float* as, int64_t as_sm,
+                          int64_t as_sk, const uint8_t* w, int64_t ldw, const float* ws,
+                          int64_t ws_sn, int64_t ws_sk, void* out, int out_dtype, int64_t ldo,
+                          int64_t M, int64_t N, int64_t K, void* workspace,
+                          size_t workspace_bytes, int config, void* stream) {
+  if (!valid_dtype(out_dtype) || M < 0 || N < 0 || K <= 0 || ldq < K || ldw < K || ldo < N)
+    return MI355X_FP8_ERR_INVALID;
+  GemmPlan plan;
+  int st = plan_gemm(M, N, K, config, &plan);
+  if (st != MI355X_FP8_OK) return st;
+  if (M == 0 || N == 0) return MI355X_FP8_OK;
+  if (!q || !as || !w || !ws || !out) return MI355X_FP8_ERR_INVALID;
+  const size_t need = gemm_workspace_bytes(plan);
+  if (need > 0 && (workspace == nullptr || workspace_bytes < need)) return MI355X_FP8_ERR_WORKSPACE;
+  return launch_block_gemm(plan, q, ldq, as, as_sm, as_sk, w, ldw, ws, ws_sn, ws_sk, out, out_dtype,
+                           ldo, M, N, K, workspace, static_cast<hipStream_t>(stream));
+}
+
+size_t mi355x_fp8_linear_workspace_bytes(int64_t M, int64_t N, int64_t K, int config) {
+  LinearLayout L;
+  if (M < 0 || N < 0 || K <= 0 || linear_layout(M, N, K, config, &L) != MI355X_FP8_OK) return 0;
+  return L.total;
+}
+
+int mi355x_fp8_linear(const void* x, int x_dtype, int64_t M, int64_t K, int64_t sxm,
+                      int64_t sxk, const uint8_t* w, int64_t ldw, const float* ws,
+                      int64_t ws_sn, int64_t ws_sk, int64_t N, void* out, int out_dtype,
+                      int64_t ldo, void* workspace, size_t workspace_bytes, int config,
+                      void* stream) {
+  if (!valid_dtype(x_dtype) || !valid_dtype(out_dtype) || M < 0 || N < 0 || K <= 0 || ldw < K || ldo < N)
+    return MI355X_FP8_ERR_INVALID;
+  LinearLayout L;
+  int st = linear_layout(M, N, K, config, &L);
+  if (st != MI355X_FP8_OK) return st;
+  if (M == 0 || N == 0) return MI355X_FP8_OK;
+  if (!x || !w || !ws || !out) return MI355X_FP8_ERR_INVALID;
+  if (workspace == nullptr || workspace_bytes < L.total) return MI355X_FP8_ERR_WORKSPACE;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  char* base = static_cast<char*>(workspace);
+  uint8_t* q = reinterpret_cast<uint8_t*>(base + L.q_off);
+  float* as = reinterpret_cast<float*>(base + L.s_off);
+  // Activation scales are stored K-group-major ([KB][Mpad]) so that GEMM lanes that own
+  // consecutive rows read consecutive scales.
+  st = launch_act_quant(x, x_dtype, M, K, sxm, sxk, q, L.kpad, L.kpad, as, 1, L.mpad, s);
+  if (st != MI355X_FP8_OK) return st;
+  return launch_block_gemm(L.plan, q, L.kpad, as, 1, L.mpad, w, ldw, ws, ws_sn, ws_sk, out, out_dtype,
+                           ldo, M, N, K, workspace, s);
+}
+
+}  // extern "C"

@@ -1,0 +1,99 @@
+// Shared device helpers for the gfx950 FP8 block-scaled linear kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mi355x {
+
+typedef int v8i __attribute__((ext_vector_type(8)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+constexpr int kGroup = 128;  // K elements per activation/weight scale group
+constexpr int kWave = 64;
+
+// Element type tags shared with the C-ABI (include/mi355x_fp8.h: MI355X_FP8_DTYPE_*).
+enum DType : int { kBF16 = 0, kF16 = 1 };
+
+struct bf16_t { uint16_t bits; };
+struct f16_t { uint16_t bits; };
+
+__device__ __forceinline__ float to_f32(bf16_t h) {
+  return __uint_as_float(static_cast<uint32_t>(h.bits) << 16);
+}
+__device__ __forceinline__ float to_f32(f16_t h) {
+  _Float16 v;
+  __builtin_memcpy(&v, &h.bits, 2);
+  return static_cast<float>(v);
+}
+
+// fp32 -> bf16 with round-to-nearest-even (NaN kept quiet).
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+// fp32 -> binary16 with the hardware's round-to-nearest-even conversion.
+__device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {
+  _Float16 v = static_cast<_Float16>(f);
+  uint16_t b;
+  __builtin_memcpy(&b, &v, 2);
+  return b;
+}
+
+template <typename T> struct OutCvt;
+template <> struct OutCvt<bf16_t> {
+  __device__ static uint16_t cvt(float f) { return f32_to_bf16_bits(f); }
+};
+template <> struct OutCvt<f16_t> {
+  __device__ static uint16_t cvt(float f) { return f32_to_f16_bits(f); }
+};
+
+// Two fp32 -> two OCP e4m3fn codes (round-to-nearest-even), packed into the low 16 bits.
+__device__ __forceinline__ uint32_t cvt_pk_e4m3(float a, float b) {
+  return static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false)) & 0xffffu;
+}
+
+// D(16x16, fp32) = A(16 x 128 e4m3) * B(128 x 16 e4m3), accumulator input zero.
+// Lane l supplies row (l % 16) of A and column (l % 16) of B; both operands place the
+// same 32 K-bytes in lane group l / 16, so the 128-long dot is complete in one
+// instruction.  Lane l receives D[4 * (l / 16) + v][l % 16] in element v.
+__device__ __forceinline__ v4f mfma_16x16x128_e4m3(v8i a, v8i b) {
+  v4f zero = {0.f, 0.f, 0.f, 0.f};
+  // cbsz = blgp = 0 selects e4m3 for both operands; zero scales select the unscaled form.
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, zero, 0, 0, 0, 0, 0, 0);
+}
+
+__device__ __forceinline__ v8i pack_v8i(uint4 lo, uint4 hi) {
+  v8i r;
+  r[0] = static_cast<int>(lo.x); r[1] = static_cast<int>(lo.y);
+  r[2] = static_cast<int>(lo.z); r[3] = static_cast<int>(lo.w);
+  r[4] = static_cast<int>(hi.x); r[5] = static_cast<int>(hi.y);
+  r[6] = static_cast<int>(hi.z); r[7] = static_cast<int>(hi.w);
+  return r;
+}
+
+// Loads 16 bytes of row `row` starting at column `k` of a byte matrix (row stride ld).
+// Bytes outside [0, rows) x [0, K) read as zero (e4m3 +0).  ALIGNED means K, ld and the
+// base pointer are multiples of 16, so a chunk is either fully inside K or fully outside
+// and one 16-byte load serves it; otherwise the chunk is assembled from byte loads.
+template <bool ALIGNED>
+__device__ __forceinline__ uint4 load_chunk16(const uint8_t* __restrict__ base, int64_t ld,
+                                              int64_t row, int64_t rows, int64_t k, int64_t K) {
+  uint4 v = make_uint4(0u, 0u, 0u, 0u);
+  if (ALIGNED) {
+    if (row < rows && k < K) v = *reinterpret_cast<const uint4*>(base + row * ld + k);
+    return v;
+  }
+  if (row >= rows) return v;
+  const uint8_t* p = base + row * ld + k;
+  uint32_t w[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    if (k + i < K) w[i >> 2] |= static_cast<uint32_t>(p[i]) << (8 * (i & 3));
+  }
+  return make_uint4(w[0], w[1], w[2], w[3]);
+}
+
+}  // namespace mi355x

@@ -1,0 +1,78 @@
+"""ctypes binding of libmi355x_fp8.so.  Fails loudly when the library is missing.
+
+torch is imported first on purpose: torch's bundled HIP runtime then owns the
+``libamdhip64.so.7`` soname, and the library binds to that same runtime, so torch's
+streams and device pointers are valid arguments.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+
+import torch  # noqa: F401  (must load the HIP runtime before the library)
+
+from .build import LIB_PATH
+
+_i64 = ctypes.c_int64
+_int = ctypes.c_int
+_ptr = ctypes.c_void_p
+_size = ctypes.c_size_t
+
+# Mirrors include/mi355x_fp8.h.
+ABI_VERSION = 1
+DTYPE_BF16 = 0
+DTYPE_F16 = 1
+CONFIG_AUTO = 0
+CONFIG_STREAM = 1
+CONFIG_TILE128 = 2
+OK = 0
+ERR_INVALID = 1
+ERR_UNSUPPORTED = 2
+ERR_WORKSPACE = 3
+ERR_LAUNCH = 4
+
+EXPORTS = {
+    "mi355x_fp8_abi_version": ([], _int),
+    "mi355x_fp8_status_string": ([_int], ctypes.c_char_p),
+    "mi355x_fp8_act_quant": ([_ptr, _int, _i64, _i64, _i64, _i64, _ptr, _i64, _i64, _ptr, _i64, _i64, _ptr], _int),
+    "mi355x_fp8_block_gemm_workspace_bytes": ([_i64, _i64, _i64, _int], _size),
+    "mi355x_fp8_block_gemm": ([_ptr, _i64, _ptr, _i64, _i64, _ptr, _i64, _ptr, _i64, _i64, _ptr, _int, _i64,
+                               _i64, _i64, _i64, _ptr, _size, _int, _ptr], _int),
+    "mi355x_fp8_linear_workspace_bytes": ([_i64, _i64, _i64, _int], _size),
+    "mi355x_fp8_linear": ([_ptr, _int, _i64, _i64, _i64, _i64, _ptr, _i64, _ptr, _i64, _i64, _i64, _ptr, _int,
+                           _i64, _ptr, _size, _int, _ptr], _int),
+}
+
+_lib = None
+
+
+def load() -> ctypes.CDLL:
+    """Load the HIP library (once).  Raises if it has not been built."""
+
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(
+                f"{LIB_PATH} is missing: build it with `python -m minillm_amd.build` "
+                "(there is no fallback implementation)")
+        lib = ctypes.CDLL(LIB_PATH)
+        for name, (args, res) in EXPORTS.items():
+            fn = getattr(lib, name)
+            fn.argtypes = args
+            fn.restype = res
+        if lib.mi355x_fp8_abi_version() != ABI_VERSION:
+            raise RuntimeError("libmi355x_fp8.so ABI version mismatch; rebuild it")
+        _lib = lib
+    return _lib
+
+
+def check(status: int) -> None:
+    """Map a C status code to the reference's exception types."""
+
+    if status == OK:
+        return
+    text = load().mi355x_fp8_status_string(status).decode()
+    if status in (ERR_INVALID, ERR_WORKSPACE):
+        raise ValueError(f"libmi355x_fp8: {text}")
+    raise RuntimeError(f"libmi355x_fp8: {text} (status {status})")

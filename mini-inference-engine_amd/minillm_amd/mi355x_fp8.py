@@ -1,0 +1,349 @@
+"""Dynamic block-scaled FP8 linear for AMD MI355X (gfx950), Transformers-compatible.
+
+Mirrors the call surface of the reference's engine/kernels/sm89_fp8.py: the same
+``fp8_linear`` signature (so ``FP8Linear.forward`` and the merged projections call it
+unchanged), the same dispatch/bucket helpers, the same exception types.  The arithmetic
+runs in two hand-written gfx950 HIP kernels behind a C-ABI (include/mi355x_fp8.h):
+
+* a per-token 1x128 activation quantizer: s = amax/448 stored raw,
+  q = e4m3fn(x / max(s, 1e-12)) -- bit-exact with the reference's quantizer;
+* a block-scaled FP8 GEMM on CDNA4 fp8 MFMA that accumulates, per 128-wide K group in
+  increasing order, dot(q, w) * a_s * w_s in fp32 and rounds once to bf16/fp16.
+
+There is no second backend: a call outside the supported set raises instead of
+delegating (the reference delegates to Transformers, sm89_fp8.py:467-481).
+"""
+
+from __future__ import annotations
+
+from collections.abc import Callable
+from dataclasses import dataclass
+from typing import Any
+
+import torch
+
+from . import _lib
+
+SUPPORTED_BLOCK_SIZE = (128, 128)
+# Same bucket cap and dispatch threshold names as sm89_fp8.py:26-34.  Both paths run
+# the same quantizer + GEMM here; the names stay for call-surface compatibility.
+MAX_M_BUCKET = 16384
+SPLIT_M_THRESHOLD = 256
+# Rows at or below which the auto GEMM choice is the weight-streaming (decode) kernel.
+STREAM_M_THRESHOLD = 64
+_original_fp8_linear: Callable[..., torch.Tensor] | None = None
+
+
+@dataclass(frozen=True)
+class FP8GemmConfig:
+    """A forced GEMM kernel choice (the reference's FP8GemmConfig, sm89_fp8.py:38-62).
+
+    ``block_k`` is fixed at 128: one K group per MFMA, so a config changes speed, never
+    the grouping of the arithmetic.
+    """
+
+    name: str
+    kernel: int
+    block_m: int
+    block_n: int
+    block_k: int = 128
+
+    @property
+    def label(self) -> str:
+        return f"{self.name}:{self.block_m}x{self.block_n}x{self.block_k}"
+
+
+GEMM_CONFIGS = (
+    FP8GemmConfig("stream", _lib.CONFIG_STREAM, 64, 64),
+    FP8GemmConfig("tile128", _lib.CONFIG_TILE128, 128, 128),
+)
+# Alias under the reference's name.
+SPLIT_GEMM_CONFIGS = GEMM_CONFIGS
+
+
+def m_bucket(rows: int) -> int:
+    """Ceiling power of two, capped at the last pre-tuned bucket (sm89_fp8.py:89-94)."""
+
+    if rows < 0:
+        raise ValueError("rows must be nonnegative")
+    return min(1 << (max(1, rows) - 1).bit_length(), MAX_M_BUCKET)
+
+
+def select_fp8_path(rows: int, path: str = "auto") -> str:
+    """Resolve dispatch; the threshold is inclusive (sm89_fp8.py:97-104)."""
+
+    if path not in {"auto", "fused", "split"}:
+        raise ValueError(f"Unknown MI355X FP8 path: {path!r}")
+    if rows < 0:
+        raise ValueError("rows must be nonnegative")
+    return ("split" if rows >= SPLIT_M_THRESHOLD else "fused") if path == "auto" else path
+
+
+def pretune_row_buckets(max_tokens: int) -> tuple[int, ...]:
+    """Every power-of-two bucket through the ceiling bucket (sm89_fp8.py:107-110)."""
+
+    return tuple(1 << i for i in range(m_bucket(max(1, max_tokens)).bit_length()))
+
+
+def mi355x_available(device: torch.device | str | int | None = None) -> bool:
+    """Whether a gfx950 GPU is visible to torch (the reference's sm89_available)."""
+
+    if not torch.cuda.is_available():
+        return False
+    props = torch.cuda.get_device_properties(device if device is not None else torch.cuda.current_device())
+    return str(getattr(props, "gcnArchName", "")).split(":")[0] == "gfx950"
+
+
+def _supports_call(input, weight, weight_scale_inv, block_size, activation_scale) -> bool:
+    """The accepted call set of sm89_fp8.py:123-147, on a gfx950 device."""
+
+    return bool(
+        input.is_cuda and weight.is_cuda and weight_scale_inv.is_cuda
+        and input.device == weight.device == weight_scale_inv.device
+        and mi355x_available(weight.device)
+        and input.dtype in {torch.float16, torch.bfloat16}
+        and weight.dtype == torch.float8_e4m3fn
+        and weight_scale_inv.dtype == torch.float32
+        and input.ndim >= 2 and weight.ndim == 2 and weight_scale_inv.ndim == 2
+        and block_size is not None and tuple(block_size) == SUPPORTED_BLOCK_SIZE
+        and activation_scale is None
+        and input.shape[-1] == weight.shape[1]
+        and tuple(weight_scale_inv.shape)
+        == ((weight.shape[0] + 127) // 128, (weight.shape[1] + 127) // 128)
+    )
+
+
+def _dtype_code(dtype: torch.dtype) -> int:
+    if dtype == torch.bfloat16:
+        return _lib.DTYPE_BF16
+    if dtype == torch.float16:
+        return _lib.DTYPE_F16
+    raise TypeError(f"unsupported dtype {dtype}")
+
+
+class _Workspace:
+    """Per (device, stream) zero-initialised byte buffer, grown on demand.
+
+    The library leaves its split-K counters at zero after every call, so a buffer is
+    zero-filled only when it is (re)allocated.  Calls on one stream are ordered, so they
+    may share it; different streams get different buffers.
+    """
+
+    def __init__(self) -> None:
+        self._buffers: dict[tuple[int, int], torch.Tensor] = {}
+
+    def get(self, device: torch.device, nbytes: int) -> torch.Tensor | None:
+        if nbytes == 0:
+            return None
+        stream = torch.cuda.current_stream(device)
+        key = (device.index if device.index is not None else torch.cuda.current_device(), stream.cuda_stream)
+        buf = self._buffers.get(key)
+        if buf is None or buf.numel() < nbytes:
+            grown = max(nbytes, 0 if buf is None else 2 * buf.numel())
+            buf = torch.zeros(grown, dtype=torch.uint8, device=device)
+            self._buffers[key] = buf
+        return buf
+
+    def clear(self) -> None:
+        self._buffers.clear()
+
+
+_workspace = _Workspace()
+
+
+def _stream_ptr(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def quantize_mi355x_fp8_activation(input_2d: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """Quantize a 2-D activation once: ``(q [M, K] e4m3fn, s [M, ceil(K/128)] fp32)``.
+
+    Same contract and errors as quantize_sm89_fp8_activation (sm89_fp8.py:401-424); the
+    input may have any strides, the outputs are contiguous and the scales raw.
+    """
+
+    if input_2d.ndim != 2 or input_2d.dtype not in {torch.bfloat16, torch.float16}:
+        raise ValueError("Expected a 2D bf16/fp16 activation")
+    if not input_2d.is_cuda or not mi355x_available(input_2d.device):
+        raise RuntimeError("Activation quantization requires an MI355X (gfx950) GPU")
+    m, k = input_2d.shape
+    if k == 0:
+        raise ValueError("Activation width must be positive")
+    groups_k = (k + 127) // 128
+    quantized = torch.empty((m, k), device=input_2d.device, dtype=torch.float8_e4m3fn)
+    scales = torch.empty((m, groups_k), device=input_2d.device, dtype=torch.float32)
+    if m:
+        _lib.check(_lib.load().mi355x_fp8_act_quant(
+            input_2d.data_ptr(), _dtype_code(input_2d.dtype), m, k, input_2d.stride(0), input_2d.stride(1),
+            quantized.data_ptr(), k, k, scales.data_ptr(), groups_k, 1, _stream_ptr(input_2d.device)))
+    return quantized, scales
+
+
+def _config_code(config: FP8GemmConfig | None) -> int:
+    return _lib.CONFIG_AUTO if config is None else config.kernel
+
+
+def launch_block_gemm(activation: torch.Tensor, weight: torch.Tensor, output: torch.Tensor,
+                      activation_scales: torch.Tensor, weight_scales: torch.Tensor,
+                      config: FP8GemmConfig | None = None) -> None:
+    """GEMM on pre-quantized activations into ``output`` (the reference's
+    _launch_split_gemm, sm89_fp8.py:427-441).  ``config`` forces a kernel."""
+
+    m, k = activation.shape
+    n = weight.shape[0]
+    for t in (activation, weight, output):
+        if t.stride(-1) != 1:
+            raise ValueError("activation, weight and output need unit column stride")
+    lib = _lib.load()
+    code = _config_code(config)
+    nbytes = lib.mi355x_fp8_block_gemm_workspace_bytes(m, n, k, code)
+    ws = _workspace.get(output.device, nbytes)
+    _lib.check(lib.mi355x_fp8_block_gemm(
+        activation.data_ptr(), activation.stride(0), activation_scales.data_ptr(),
+        activation_scales.stride(0), activation_scales.stride(1), weight.data_ptr(), weight.stride(0),
+        weight_scales.data_ptr(), weight_scales.stride(0), weight_scales.stride(1), output.data_ptr(),
+        _dtype_code(output.dtype), output.stride(0), m, n, k,
+        None if ws is None else ws.data_ptr(), 0 if ws is None else ws.numel(), code,
+        _stream_ptr(output.device)))
+
+
+def mi355x_fp8_linear(
+    input: torch.Tensor,
+    weight: torch.Tensor,
+    weight_scale_inv: torch.Tensor,
+    block_size: list[int] | tuple[int, int] | None = None,
+    bias: torch.Tensor | None = None,
+    activation_scale: torch.Tensor | None = None,
+    output_dtype: torch.dtype | None = None,
+    allow_deepgemm: bool = True,
+    *,
+    path: str = "auto",
+    gemm_config: FP8GemmConfig | None = None,
+) -> torch.Tensor:
+    """Transformers-compatible FP8 linear (the reference's sm89_fp8_linear,
+    sm89_fp8.py:444-528).
+
+    ``path`` accepts "auto", "fused" and "split" (all three run the quantizer + block
+    GEMM); ``gemm_config`` requires ``path="split"`` and forces the GEMM kernel.
+    ``allow_deepgemm`` is accepted and ignored, as in the reference's fast path.
+    """
+
+    select_fp8_path(0, path)  # reject typos first
+    if gemm_config is not None and (path != "split" or gemm_config not in GEMM_CONFIGS):
+        raise ValueError("gemm_config must be a listed GEMM config with path='split'")
+    if not _supports_call(input, weight, weight_scale_inv, block_size, activation_scale):
+        raise RuntimeError(
+            "Unsupported MI355X FP8 call (needs gfx950 tensors, bf16/fp16 input, e4m3fn weight, "
+            "fp32 [ceil(N/128), ceil(K/128)] scales, block_size (128, 128), no activation_scale); "
+            "there is no fallback backend")
+    if output_dtype is not None and output_dtype not in {torch.float16, torch.bfloat16}:
+        raise TypeError("MI355X FP8 output must be float16 or bfloat16")
+
+    k = int(input.shape[-1])
+    m = int(input.numel() // k) if k else 0
+    n = int(weight.shape[0])
+    out_dtype = output_dtype or input.dtype
+    output = torch.empty((m, n), device=input.device, dtype=out_dtype)
+    select_fp8_path(m, path)
+    if m == 0 or n == 0:
+        result = output.reshape(*input.shape[:-1], n)
+        return result if bias is None else result + bias
+    if k == 0:
+        raise ValueError("Activation width must be positive")
+    input_2d = input.reshape(m, k)
+    if input_2d.stride(-1) != 1:
+        input_2d = input_2d.contiguous()
+    weight_2d = weight if weight.stride(-1) == 1 else weight.contiguous()
+    scales_2d = weight_scale_inv
+    lib = _lib.load()
+    code = _config_code(gemm_config)
+    nbytes = lib.mi355x_fp8_linear_workspace_bytes(m, n, k, code)
+    ws = _workspace.get(input.device, nbytes)
+    _lib.check(lib.mi355x_fp8_linear(
+        input_2d.data_ptr(), _dtype_code(input_2d.dtype), m, k, input_2d.stride(0), input_2d.stride(1),
+        weight_2d.data_ptr(), weight_2d.stride(0), scales_2d.data_ptr(), scales_2d.stride(0),
+        scales_2d.stride(1), n, output.data_ptr(), _dtype_code(out_dtype), output.stride(0),
+        ws.data_ptr(), ws.numel(), code, _stream_ptr(input.device)))
+    result = output.reshape(*input.shape[:-1], n)
+    return result if bias is None else result + bias
+
+
+# The name Transformers' FP8Linear calls.
+fp8_linear = mi355x_fp8_linear
+
+
+def pretune_mi355x_fp8(model: Any, max_tokens: int = MAX_M_BUCKET) -> int:
+    """Warm every (shape, row bucket) pair of a model's FP8 linears (sm89_fp8.py:531-558).
+
+    There is no autotuner to run: kernel choice is a closed-form function of the shape.
+    Warming sizes each stream's workspace for the largest bucket so that later calls
+    (including ones under HIP-graph capture) allocate nothing.  Returns the number of
+    shape/bucket pairs.
+    """
+
+    shapes = {
+        (module.weight, module.weight_scale_inv, tuple(getattr(module, "block_size", SUPPORTED_BLOCK_SIZE)))
+        for module in model.modules()
+        if getattr(getattr(module, "weight", None), "dtype", None) == torch.float8_e4m3fn
+        and isinstance(getattr(module, "weight_scale_inv", None), torch.Tensor)
+    }
+    dtype = next(p.dtype for p in model.parameters() if p.dtype in {torch.bfloat16, torch.float16})
+    return pretune_mi355x_fp8_shapes(shapes, dtype, max_tokens)
+
+
+def pretune_mi355x_fp8_shapes(shapes: Any, dtype: torch.dtype, max_tokens: int = MAX_M_BUCKET) -> int:
+    """``pretune_mi355x_fp8`` for explicit ``(weight, scales, block_size)`` triples."""
+
+    unique = {}
+    for weight, scales, block in shapes:
+        unique.setdefault(tuple(weight.shape), (weight, scales, tuple(block)))
+    buckets = pretune_row_buckets(int(max_tokens))
+    with torch.inference_mode():
+        for weight, scales, block in unique.values():
+            for bucket in buckets:
+                activation = torch.zeros((bucket, weight.shape[1]), dtype=dtype, device=weight.device)
+                for rows in (bucket, bucket - 1) if bucket >= 16 else (bucket,):
+                    for path in ("fused", "split"):
+                        mi355x_fp8_linear(activation[:rows], weight, scales, block_size=list(block), path=path)
+    torch.cuda.synchronize()
+    return len(unique) * len(buckets)
+
+
+def install_mi355x_fp8_dispatch() -> dict[str, Any]:
+    """Swap Transformers' ``finegrained_fp8.fp8_linear`` for this op (sm89_fp8.py:579-610)."""
+
+    if not mi355x_available():
+        arch = (str(torch.cuda.get_device_properties(torch.cuda.current_device()).gcnArchName)
+                if torch.cuda.is_available() else None)
+        raise RuntimeError(f"The custom FP8 kernel requires an AMD gfx950 (MI355X) GPU; detected arch={arch}")
+    _lib.load()
+    from transformers.integrations import finegrained_fp8
+
+    global _original_fp8_linear
+    if finegrained_fp8.fp8_linear is not mi355x_fp8_linear:
+        _original_fp8_linear = finegrained_fp8.fp8_linear
+        finegrained_fp8.fp8_linear = mi355x_fp8_linear
+    return {
+        "installed": True,
+        "backend": "minillm_mi355x_hip_fp8",
+        "arch_required": "gfx950",
+        "block_size": [128, 128],
+        "fused_operations": [
+            "dynamic activation scaling",
+            "FP8 E4M3 activation quantization",
+            "block-scaled FP8 matrix multiplication",
+        ],
+        "fallback": None,
+    }
+
+
+def uninstall_mi355x_fp8_dispatch() -> None:
+    """Restore the ``fp8_linear`` that ``install_mi355x_fp8_dispatch`` replaced."""
+
+    global _original_fp8_linear
+    if _original_fp8_linear is None:
+        return
+    from transformers.integrations import finegrained_fp8
+
+    finegrained_fp8.fp8_linear = _original_fp8_linear
+    _original_fp8_linear = None

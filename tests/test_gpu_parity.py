@@ -1,0 +1,204 @@
+"""GPU parity: the HIP quantizer and GEMM (through the C-ABI) against the CPU oracle.
+
+Quantized codes and scales must be bit-exact; GEMM outputs must be within the stated
+row tolerance (tests/_helpers.py: REL_TOL) of the fp32 oracle.  Inputs come from the
+CPU generator, so both sides see identical bytes.
+"""
+
+import sys
+
+import pytest
+import torch
+
+from _helpers import assert_close_rows, oracle_gemm, oracle_linear, oracle_quant
+from minillm_amd import mi355x_fp8 as fp8
+from minillm_amd.validation import (
+    MODEL_SHAPES, QWEN3_4B_PROJECTIONS, SEED, TAIL_SHAPES, ModelShape, bit_mismatch_details,
+    bitwise_equal, make_activations, make_baseline_activations, make_baseline_weights, make_weights,
+)
+
+pytestmark = pytest.mark.gpu
+
+_weights_cache = {}
+
+
+def baseline_weights(shape):
+    if shape not in _weights_cache:
+        _weights_cache[shape] = make_baseline_weights(shape, SEED)
+    return _weights_cache[shape]
+
+BLOCK = [128, 128]
+
+
+def _note(*parts):
+    print("CASE", *parts, flush=True, file=sys.stderr)
+
+
+@pytest.mark.parametrize("k", [1, 127, 128, 129, 259, 2560, 4096, 9728])
+@pytest.mark.parametrize("rows", [1, 7, 17, 100])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_quantizer_bit_exact(gpu, k, rows, dtype):
+    _note("quant", k, rows, dtype)
+    x = make_activations(rows, k, SEED, dtype)
+    q, s = fp8.quantize_mi355x_fp8_activation(x.to(gpu))
+    q_ref, s_ref = oracle_quant(x)
+    assert bitwise_equal(q.cpu(), q_ref), bit_mismatch_details(q.cpu(), q_ref)
+    assert bitwise_equal(s.cpu(), s_ref), bit_mismatch_details(s.cpu(), s_ref)
+
+
+def test_quantizer_special_rows_and_row_independence(gpu):
+    x = make_activations(7, 259, 42).to(gpu)
+    q, scales = fp8.quantize_mi355x_fp8_activation(x)
+    assert scales[1].count_nonzero().item() == 0           # zero row: raw zero scales
+    assert (scales[3] < 1e-12).all().item()                 # tiny row: below the clamp
+    assert (q[5].cpu().view(torch.uint8) == 0x80).all()     # -0.0 row keeps the sign
+    assert set(q[6].cpu().view(torch.uint8).tolist()) == {0x7E, 0xFE}
+    assert (scales[6] == 1.0).all().item()
+    for row in range(7):
+        q1, s1 = fp8.quantize_mi355x_fp8_activation(x[row:row + 1])
+        assert bitwise_equal(q1, q[row:row + 1])
+        assert bitwise_equal(s1, scales[row:row + 1])
+
+
+def test_quantizer_strided_input(gpu):
+    x = make_activations(9, 600, 7)
+    column_major = x.to(gpu).t().contiguous().t()
+    assert column_major.stride() == (1, 9)
+    q, s = fp8.quantize_mi355x_fp8_activation(column_major)
+    q_ref, s_ref = oracle_quant(x)
+    assert bitwise_equal(q.cpu(), q_ref) and bitwise_equal(s.cpu(), s_ref)
+
+
+def test_quantizer_subnormal_and_rounding_midpoints(gpu):
+    # Values whose quotient lands on e4m3 rounding midpoints and in its subnormal range,
+    # plus bf16 subnormal inputs.
+    base = torch.tensor([448.0, 1.0, 1.0625, 1.1875, 0.0087890625, 0.0029296875, -0.0009765625,
+                         0.001953125 * 1.5, 3.0e-39, -1.0e-38, 1e-20, 240.0, 232.0, 248.0], dtype=torch.float32)
+    x = torch.zeros((3, 256), dtype=torch.float32)
+    x[0, :base.numel()] = base
+    x[1, :base.numel()] = base * 3.0
+    x[2, 128:128 + base.numel()] = base * 1e-30
+    xb = x.to(torch.bfloat16)
+    q, s = fp8.quantize_mi355x_fp8_activation(xb.to(gpu))
+    q_ref, s_ref = oracle_quant(xb)
+    assert bitwise_equal(q.cpu(), q_ref), bit_mismatch_details(q.cpu(), q_ref)
+    assert bitwise_equal(s.cpu(), s_ref), bit_mismatch_details(s.cpu(), s_ref)
+
+
+@pytest.mark.parametrize("shape", TAIL_SHAPES + (ModelShape("kv", 1024, 2560), ModelShape("o", 2560, 4096)),
+                         ids=lambda s: s.name)
+@pytest.mark.parametrize("rows", [1, 7, 64, 65, 129, 300])
+def test_linear_matches_oracle(gpu, shape, rows):
+    _note("linear", shape, rows)
+    x = make_activations(rows, shape.k, SEED)
+    w, ws = make_weights(shape, SEED)
+    out = fp8.mi355x_fp8_linear(x.to(gpu), w.to(gpu), ws.to(gpu), BLOCK)
+    torch.cuda.synchronize()
+    assert_close_rows(out, oracle_linear(x, w, ws))
+
+
+@pytest.mark.parametrize("config", fp8.GEMM_CONFIGS, ids=lambda c: c.name)
+@pytest.mark.parametrize("shape", [TAIL_SHAPES[3], ModelShape("o", 2560, 4096), ModelShape("down", 2560, 9728)],
+                         ids=lambda s: s.name)
+@pytest.mark.parametrize("rows", [1, 16, 33, 130])
+def test_forced_configs_match_oracle_and_are_row_independent(gpu, config, shape, rows):
+    _note("forced", config.name, shape, rows)
+    x = make_activations(rows, shape.k, SEED)
+    w, ws = make_weights(shape, SEED)
+    xg, wg, wsg = x.to(gpu), w.to(gpu), ws.to(gpu)
+    out = fp8.mi355x_fp8_linear(xg, wg, wsg, BLOCK, path="split", gemm_config=config)
+    assert_close_rows(out, oracle_linear(x, w, ws))
+    for row in sorted({0, 1, 2, 5, 6, rows - 1} & set(range(rows))):
+        single = fp8.mi355x_fp8_linear(xg[row:row + 1], wg, wsg, BLOCK, path="split", gemm_config=config)
+        assert bitwise_equal(single, out[row:row + 1]), (row, bit_mismatch_details(single, out[row:row + 1]))
+
+
+@pytest.mark.parametrize("config", fp8.GEMM_CONFIGS, ids=lambda c: c.name)
+def test_gemm_entry_on_prequantized_input(gpu, config):
+    shape = ModelShape("tail", 193, 259)
+    x = make_activations(40, shape.k, 5)
+    w, ws = make_weights(shape, 5)
+    q, s = fp8.quantize_mi355x_fp8_activation(x.to(gpu))
+    out = torch.empty((40, shape.n), dtype=torch.bfloat16, device=gpu)
+    fp8.launch_block_gemm(q, w.to(gpu), out, s, ws.to(gpu), config)
+    assert_close_rows(out, oracle_gemm(q.cpu(), s.cpu(), w, ws))
+
+
+@pytest.mark.parametrize("output_dtype", [torch.bfloat16, torch.float16])
+def test_bias_output_dtype_and_flattened_input(gpu, output_dtype):
+    x = make_activations(6, 259, 42).reshape(2, 3, 259)
+    w, ws = make_weights(ModelShape("tail", 193, 259), 42)
+    bias = torch.linspace(-1, 1, 193, dtype=output_dtype)
+    out = fp8.mi355x_fp8_linear(x.to(gpu), w.to(gpu), ws.to(gpu), BLOCK, bias=bias.to(gpu),
+                                output_dtype=output_dtype)
+    assert out.shape == (2, 3, 193) and out.dtype == output_dtype
+    expected = oracle_linear(x, w, ws, output_dtype) + bias
+    assert_close_rows(out, expected)
+
+
+def test_fp16_input(gpu):
+    x = make_activations(20, 2560, 3, torch.float16)
+    w, ws = make_weights(ModelShape("kv", 1024, 2560), 3)
+    out = fp8.mi355x_fp8_linear(x.to(gpu), w.to(gpu), ws.to(gpu), BLOCK)
+    assert out.dtype == torch.float16
+    assert_close_rows(out, oracle_linear(x, w, ws))
+
+
+def test_empty_rows_and_repeatability(gpu):
+    w, ws = make_weights(ModelShape("kv", 1024, 2560), 1)
+    wg, wsg = w.to(gpu), ws.to(gpu)
+    empty = fp8.mi355x_fp8_linear(torch.empty((0, 2560), dtype=torch.bfloat16, device=gpu), wg, wsg, BLOCK)
+    assert empty.shape == (0, 1024)
+    x = make_activations(8, 2560, 1).to(gpu)
+    first = fp8.mi355x_fp8_linear(x, wg, wsg, BLOCK)
+    for _ in range(3):  # split-K counters must be back at zero after every call
+        assert bitwise_equal(fp8.mi355x_fp8_linear(x, wg, wsg, BLOCK), first)
+
+
+@pytest.mark.parametrize("shape", QWEN3_4B_PROJECTIONS, ids=lambda s: s.name)
+@pytest.mark.parametrize("rows", [1, 8, 32])
+def test_decode_shapes_baseline_data(gpu, shape, rows):
+    _note("decode", shape, rows)
+    x = make_baseline_activations(rows, shape.k, SEED)
+    w, ws = baseline_weights(shape)
+    out = fp8.mi355x_fp8_linear(x.to(gpu), w.to(gpu), ws.to(gpu), BLOCK)
+    assert_close_rows(out, oracle_linear(x, w, ws))
+
+
+def _dense(x, w, ws, n, k):
+    expanded = ws.double().repeat_interleave(128, 0).repeat_interleave(128, 1)[:n, :k]
+    return x.double() @ (w.double() * expanded).T
+
+
+def _rel_l2(out, ref):
+    return (torch.linalg.vector_norm(out.double() - ref, dim=-1)
+            / torch.linalg.vector_norm(ref, dim=-1).clamp_min(1e-12))
+
+
+@pytest.mark.parametrize("shape", QWEN3_4B_PROJECTIONS, ids=lambda s: s.name)
+def test_prefill_2048_full_size(gpu, shape):
+    """M = 2048 with outlier channels, at full size:
+    * the quantizer's codes and scales, bit-exact against the oracle on every row;
+    * every output row within REL_TOL of the fp64 product of the dequantized operands
+      (the oracle's arithmetic without its fp32 rounding);
+    * sampled rows against the oracle itself (its rows are independent);
+    * the reference judge's metric (per-row rel-L2 against the fp64 product with
+      unquantized activations) no worse than 1.25x the oracle's on the same rows."""
+
+    _note("prefill", shape)
+    rows = 2048
+    x = make_baseline_activations(rows, shape.k, SEED, outliers=True)
+    w, ws = baseline_weights(shape)
+    xg, wg, wsg = x.to(gpu), w.to(gpu), ws.to(gpu)
+    q, s = fp8.quantize_mi355x_fp8_activation(xg)
+    q_ref, s_ref = oracle_quant(x)
+    assert bitwise_equal(q.cpu(), q_ref) and bitwise_equal(s.cpu(), s_ref)
+    out = fp8.mi355x_fp8_linear(xg, wg, wsg, BLOCK)
+    a_deq = q.double() * s.double().repeat_interleave(128, 1)[:, :shape.k]
+    assert_close_rows(out, _dense(a_deq, wg, wsg, shape.n, shape.k))
+    sample = [0, 1, 2, 511, 1024, 2047]
+    expected = oracle_linear(x[sample], w, ws)
+    assert_close_rows(out[sample], expected)
+    dense = _dense(xg[sample], wg, wsg, shape.n, shape.k)
+    ours, oracle_err = _rel_l2(out[sample], dense), _rel_l2(expected.to(gpu), dense)
+    assert (ours <= 1.25 * oracle_err + 1e-4).all(), (ours.tolist(), oracle_err.tolist())
