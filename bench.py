@@ -10,10 +10,12 @@ merged Qwen3-4B projections (qkv, o_proj, gate_up, down), on one GPU.
   are resident in HBM.
 * Weights rotate through enough independent sets (> 512 MB) that no step reads weights
   that are still in the 256 MB MALL from the step before.
-* Timing uses HIP events on the stream the kernels run on (torch's current stream), per
-  launch, so ``roofline.achieved`` is the average per-launch rate of the dominant kernel.
+* Timing: each projection's launches (one per weight set) are captured in a HIP graph
+  and replayed K times between two HIP events recorded on the stream the kernels run on;
+  the per-launch time is the elapsed time over K x sets launches, so
+  ``roofline.achieved`` is the average per-launch rate of the dominant kernel.
 * ``cpu_baseline`` times the C oracle (a CPU restatement of the reference arithmetic) on
-  a bounded sample: the same four projections at M=32 rows.
+  a bounded sample: the same four projections at ``--cpu-rows`` rows.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
 """
@@ -23,7 +25,6 @@ from __future__ import annotations
 import argparse
 import json
 import os
-import statistics
 import sys
 import time
 
@@ -81,57 +82,71 @@ def main(argv=None) -> int:
         for p in projs:
             x = make_baseline_activations(m, p.k, SEED, outliers=outliers, device="cuda")
             xs.append(x)
-            qs.append(fp8.quantize_mi355x_fp8_activation(x))
+            qs.append(fp8.quantize_mi355x_fp8_activation(x, scale_layout="kgroup"))
             out.append(torch.empty((m, p.n), dtype=torch.bfloat16, device=dev))
         return xs, qs, out
 
     def run_phase(m, outliers):
+        """Per projection: one HIP graph of `sets` back-to-back GEMM launches (one per
+        weight set), replayed `steps` times between two HIP events on the launch stream.
+        Graph replay removes the host's launch gaps, so the events time the kernels."""
+
         xs, qs, outs = prepare(m, outliers)
-        # Warm up (also sizes the workspace, so the timed region allocates nothing).
-        for step in range(args.warmup):
+        stream = torch.cuda.Stream()
+        per_launch_ms, graphs = [], []
+        with torch.cuda.stream(stream):
             for i, p in enumerate(projs):
-                w, ws = weights[step % sets][i]
-                fp8.launch_block_gemm(qs[i][0], w, outs[i], qs[i][1], ws)
-        starts = [[torch.cuda.Event(enable_timing=True) for _ in projs] for _ in range(args.steps)]
-        ends = [[torch.cuda.Event(enable_timing=True) for _ in projs] for _ in range(args.steps)]
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        for step in range(args.steps):
+                for r in range(sets):  # eager warm-up outside capture
+                    fp8.launch_block_gemm(qs[i][0], weights[r][i][0], outs[i], qs[i][1], weights[r][i][1])
+                stream.synchronize()
+                graph = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(graph, stream=stream):
+                    for r in range(sets):
+                        fp8.launch_block_gemm(qs[i][0], weights[r][i][0], outs[i], qs[i][1], weights[r][i][1])
+                graphs.append(graph)
             for i, p in enumerate(projs):
-                w, ws = weights[step % sets][i]
-                starts[step][i].record()
-                fp8.launch_block_gemm(qs[i][0], w, outs[i], qs[i][1], ws)
-                ends[step][i].record()
+                for _ in range(args.warmup):
+                    graphs[i].replay()
+                start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                stream.synchronize()
+                start.record(stream)
+                for _ in range(args.steps):
+                    graphs[i].replay()
+                end.record(stream)
+                end.synchronize()
+                per_launch_ms.append(start.elapsed_time(end) / (args.steps * sets))
+            # Quantizer timing (separate: not part of the GEMM metric).
+            quant_ms = []
+            for i, p in enumerate(projs):
+                fp8.quantize_mi355x_fp8_activation(xs[i], scale_layout="kgroup")
+                graph = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(graph, stream=stream):
+                    for _ in range(sets):
+                        fp8.quantize_mi355x_fp8_activation(xs[i], scale_layout="kgroup")
+                graph.replay()
+                start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                stream.synchronize()
+                start.record(stream)
+                for _ in range(args.steps):
+                    graph.replay()
+                end.record(stream)
+                end.synchronize()
+                quant_ms.append(start.elapsed_time(end) / (args.steps * sets))
         torch.cuda.synchronize()
-        wall = time.perf_counter() - t0
-        per = [[starts[s][i].elapsed_time(ends[s][i]) for s in range(args.steps)] for i in range(len(projs))]
-        # Quantizer timing (separate: not part of the GEMM metric).
-        qstart, qend = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        quant_ms = []
-        for i, p in enumerate(projs):
-            qstart.record()
-            for _ in range(args.steps):
-                fp8.quantize_mi355x_fp8_activation(xs[i])
-            qend.record()
-            torch.cuda.synchronize()
-            quant_ms.append(qstart.elapsed_time(qend) / args.steps)
-        return per, wall, quant_ms
+        return per_launch_ms, quant_ms
 
     results = {}
     for phase, m, outliers in (("prefill", args.prefill_m, True), ("decode", args.decode_m, False)):
         print(f"timing {phase} M={m}", file=sys.stderr, flush=True)
-        per, wall, quant_ms = run_phase(m, outliers)
-        med = [statistics.median(v) for v in per]
-        mean = [statistics.fmean(v) for v in per]
+        mean, quant_ms = run_phase(m, outliers)
         flops = [linear_flops(m, p.n, p.k) for p in projs]
         nbytes = [gemm_bytes(m, p.n, p.k) for p in projs]
         results[phase] = {
             "m": m,
             "step_ms": sum(mean),
-            "wall_ms_per_step": 1e3 * wall / args.steps,
             "tflops": sum(flops) / (sum(mean) * 1e9),
             "gbps": sum(nbytes) / (sum(mean) * 1e6),
-            "per_proj": {p.name: {"median_us": 1e3 * med[i], "mean_us": 1e3 * mean[i],
+            "per_proj": {p.name: {"mean_us": 1e3 * mean[i],
                                   "tflops": flops[i] / (mean[i] * 1e9), "gbps": nbytes[i] / (mean[i] * 1e6)}
                          for i, p in enumerate(projs)},
             "quant": {p.name: {"us": 1e3 * quant_ms[i], "gbps": quant_bytes(m, p.k) / (quant_ms[i] * 1e6)}

@@ -32,6 +32,8 @@ extern "C" {
 #define MI355X_FP8_CONFIG_AUTO 0
 #define MI355X_FP8_CONFIG_STREAM 1  /* weight-streaming split-K kernel, M <= 64 */
 #define MI355X_FP8_CONFIG_TILE128 2 /* LDS-tiled 128x128 MFMA kernel, any M */
+#define MI355X_FP8_CONFIG_TILE256 3 /* 256x256 MFMA kernel; needs K % 128 == 0, 16-byte
+                                       aligned q/w and K-group-major activation scales */
 
 /* Status codes. */
 #define MI355X_FP8_OK 0
@@ -60,12 +62,9 @@ int mi355x_fp8_act_quant(const void* x, int x_dtype, int64_t M, int64_t K, int64
                          int64_t s_sm, int64_t s_sk, void* stream);
 
 /*
- * Workspace bytes that mi355x_fp8_block_gemm needs for (M, N, K, config).  Every
- * workspace begins with a fixed 256 KiB region of split-K arrival counters, so the size is
- * never below 256 KiB.  That region must be zero-filled once when the workspace is
- * allocated; every call leaves it zero again, so one workspace can be reused, for any
- * shapes, by calls that are ordered on one stream.  Calls that overlap in time must not
- * share a workspace.
+ * Workspace bytes that mi355x_fp8_block_gemm needs for (M, N, K, config); 0 when the
+ * chosen kernels need none (the current ones).  A workspace is scratch: its contents need
+ * no initialisation, and calls that overlap in time must not share one.
  */
 size_t mi355x_fp8_block_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int config);
 
@@ -84,8 +83,8 @@ int mi355x_fp8_block_gemm(const uint8_t* q, int64_t ldq, const float* as, int64_
                           int64_t M, int64_t N, int64_t K, void* workspace,
                           size_t workspace_bytes, int config, void* stream);
 
-/* Workspace bytes that mi355x_fp8_linear needs (quantized activations, their scales and
- * the GEMM's workspace).  Same zero-once / reuse rules as the GEMM workspace. */
+/* Workspace bytes that mi355x_fp8_linear needs: the quantized activations, their scales
+ * and the GEMM's workspace.  Same rules as the GEMM workspace. */
 size_t mi355x_fp8_linear_workspace_bytes(int64_t M, int64_t N, int64_t K, int config);
 
 /*

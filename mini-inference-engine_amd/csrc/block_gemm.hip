@@ -16,12 +16,11 @@
 //
 // Two kernels:
 //   stream_gemm_kernel  decode-sized M (<= 64 rows per launch slice).  HBM-bound weight
-//                       streaming: W goes global -> registers (each byte read once), the
-//                       small activation matrix is served from L2.  Grid = 64-row W strips x
-//                       K splits; the 4 waves of a workgroup take interleaved K groups and
-//                       reduce through LDS; K splits reduce through an fp32 workspace, the
-//                       last-arriving workgroup of a strip summing the partials in split
-//                       order (deterministic) and resetting the strip's counter.
+//                       streaming: each workgroup owns 16 or 32 W rows over the whole of
+//                       K, W goes global -> registers (every byte read once, D K groups in
+//                       flight per wave), the small activation matrix is served from L2,
+//                       and the eight waves' K-partials combine in LDS.  No workspace, no
+//                       cross-workgroup synchronisation.
 //   tile_gemm_kernel    prefill-sized M.  MFMA-bound: 128x128 output tile per 256-thread
 //                       workgroup, 2x2 waves of 64x64, K groups staged global -> registers
 //                       -> LDS with double buffering and an XOR-swizzled (conflict-free)
@@ -31,154 +30,109 @@
 
 namespace mi355x {
 
-constexpr int kThreads = 256;
-constexpr int kStripRows = 64;           // W rows per stream-kernel workgroup
-constexpr int kRedStride = kStripRows + 4;
+constexpr int kThreads = 256;  // tile kernel
 
 // ------------------------------------------------------------------------------------
 // Stream kernel (decode M)
 // ------------------------------------------------------------------------------------
-template <int NT, bool ALIGNED, typename OutT>
-__global__ __launch_bounds__(kThreads) void stream_gemm_kernel(
+// One workgroup owns 16*AF consecutive W rows and reads them over the whole of K exactly
+// once.  Its WAVES waves take K groups round-robin (wave w: w, w + WAVES, ...), each
+// keeping D groups of loads in flight, and combine their fp32 partials through LDS in
+// wave order.  The assignment of K groups to waves depends on K alone, so a row's result
+// is the same whatever M is or whichever projections are concatenated along N.
+constexpr int kStreamWaves = 8;
+constexpr int kStreamDepth = 2;
+
+template <int NT, int AF, bool ALIGNED, typename OutT>
+__global__ __launch_bounds__(kStreamWaves * 64) void stream_gemm_kernel(
     const uint8_t* __restrict__ q, int64_t ldq, const float* __restrict__ as, int64_t as_sm,
     int64_t as_sk, const uint8_t* __restrict__ w, int64_t ldw, const float* __restrict__ ws,
     int64_t ws_sn, int64_t ws_sk, uint16_t* __restrict__ out, int64_t ldo, int64_t M, int64_t N,
-    int64_t K, int64_t KB, int64_t kb_per_split, int64_t splits, float* __restrict__ partials,
-    unsigned* __restrict__ counters) {
-  constexpr int kTok = 16 * NT;                      // token rows of this slice
-  constexpr int kElems = kTok * kStripRows;          // outputs per workgroup
-  __shared__ float red[2 * kTok * kRedStride];
-  __shared__ int is_last;
+    int64_t K, int64_t KB) {
+  constexpr int kRows = 16 * AF;            // W rows of this workgroup
+  constexpr int kTok = 16 * NT;             // token rows of this slice
+  constexpr int kStride = kRows + 4;        // padded LDS row (floats)
+  __shared__ float red[kStreamWaves * kTok * kStride];
 
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
   const int lane = tid & 63;
   const int r = lane & 15;
   const int g = lane >> 4;
-  const int64_t strip = blockIdx.x;
-  const int64_t split = blockIdx.y;
-  const int64_t tslice = blockIdx.z;
-  const int64_t n0 = strip * kStripRows;
-  const int64_t m_base = tslice * 64;
+  const int64_t n0 = static_cast<int64_t>(blockIdx.x) * kRows;
+  const int64_t m_base = static_cast<int64_t>(blockIdx.z) * 64;
   const int64_t m_rows = (M - m_base) < kTok ? (M - m_base) : kTok;
-  const int64_t kb_begin = split * kb_per_split;
-  const int64_t kb_end = (kb_begin + kb_per_split) < KB ? (kb_begin + kb_per_split) : KB;
   const int64_t nb = n0 / kGroup;
 
-  v4f acc[4][NT];
+  v4f acc[AF][NT];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < AF; ++i)
 #pragma unroll
     for (int j = 0; j < NT; ++j) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
 
-  for (int64_t kb = kb_begin + wave; kb < kb_end; kb += 4) {
-    const int64_t k_lo = kb * kGroup + 16 * g;
-    const int64_t k_hi = k_lo + 64;
-    v8i a[4];
+  // The wave index is uniform across the wave: make that visible to the compiler so that
+  // the K-group bookkeeping and the weight-scale loads stay scalar.
+  const int64_t wave_u = __builtin_amdgcn_readfirstlane(wave);
+  for (int64_t kb0 = wave_u; kb0 < KB; kb0 += kStreamWaves * kStreamDepth) {
+    v8i a[kStreamDepth][AF];
+    v8i b[kStreamDepth][NT];
+    float asv[kStreamDepth][NT];
+    float wsv[kStreamDepth];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int64_t row = n0 + 16 * i + r;
-      a[i] = pack_v8i(load_chunk16<ALIGNED>(w, ldw, row, N, k_lo, K),
-                      load_chunk16<ALIGNED>(w, ldw, row, N, k_hi, K));
-    }
-    v8i b[NT];
-    float sc[NT];
-    const float wsv = ws[nb * ws_sn + kb * ws_sk];
+    for (int d = 0; d < kStreamDepth; ++d) {
+      const int64_t kb = kb0 + d * kStreamWaves;
+      const int64_t kbc = kb < KB ? kb : KB - 1;  // clamped: loads stay in bounds, result unused
+      const int64_t k_lo = kbc * kGroup + 16 * g;
 #pragma unroll
-    for (int j = 0; j < NT; ++j) {
-      const int64_t tok = 16 * j + r;
-      const int64_t m = m_base + tok;
-      b[j] = pack_v8i(load_chunk16<ALIGNED>(q, ldq, m, M, k_lo, K),
-                      load_chunk16<ALIGNED>(q, ldq, m, M, k_hi, K));
-      sc[j] = (tok < m_rows ? as[m * as_sm + kb * as_sk] : 0.0f) * wsv;
-    }
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
+      for (int i = 0; i < AF; ++i) {
+        const int64_t row = n0 + 16 * i + r;
+        a[d][i] = pack_v8i(load_chunk16<ALIGNED>(w, ldw, row, N, k_lo, K),
+                           load_chunk16<ALIGNED>(w, ldw, row, N, k_lo + 64, K));
+      }
+      wsv[d] = ws[nb * ws_sn + kbc * ws_sk];
 #pragma unroll
       for (int j = 0; j < NT; ++j) {
-        const v4f d = mfma_16x16x128_e4m3(a[i], b[j]);
-#pragma unroll
-        for (int v = 0; v < 4; ++v) acc[i][j][v] = __builtin_fmaf(d[v], sc[j], acc[i][j][v]);
+        const int64_t tok = 16 * j + r;
+        const int64_t m = m_base + tok;
+        b[d][j] = pack_v8i(load_chunk16<ALIGNED>(q, ldq, m, M, k_lo, K),
+                           load_chunk16<ALIGNED>(q, ldq, m, M, k_lo + 64, K));
+        asv[d][j] = tok < m_rows ? as[m * as_sm + kbc * as_sk] : 0.0f;
       }
-  }
-
-  // Lane holds D[n = 16 i + 4 g + v][token = 16 j + r].  Combine the four waves as
-  // (w0 + w1) + (w2 + w3) through two LDS slots laid out [token][n] (fixed order, so the
-  // result does not depend on wave timing), leaving the sum in slot A.
-  float* slot_a = red;
-  float* slot_b = red + kTok * kRedStride;
-  auto put = [&](float* slot) {
+    }
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int d = 0; d < kStreamDepth; ++d) {
+      if (kb0 + d * kStreamWaves >= KB) break;
 #pragma unroll
-      for (int j = 0; j < NT; ++j)
-        *reinterpret_cast<float4*>(slot + (16 * j + r) * kRedStride + 16 * i + 4 * g) =
-            make_float4(acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]);
-  };
-  auto add = [&](const float* slot) {
+      for (int i = 0; i < AF; ++i)
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+        for (int j = 0; j < NT; ++j) {
+          const v4f p = mfma_16x16x128_e4m3(a[d][i], b[d][j]);
+          const float sc = asv[d][j] * wsv[d];
 #pragma unroll
-      for (int j = 0; j < NT; ++j) {
-        const float4 t = *reinterpret_cast<const float4*>(slot + (16 * j + r) * kRedStride + 16 * i + 4 * g);
-        acc[i][j][0] += t.x; acc[i][j][1] += t.y; acc[i][j][2] += t.z; acc[i][j][3] += t.w;
-      }
-  };
-  if (wave == 1) put(slot_a);
-  if (wave == 3) put(slot_b);
-  __syncthreads();
-  if (wave == 0) add(slot_a);
-  if (wave == 2) add(slot_b);
-  __syncthreads();
-  if (wave == 2) put(slot_a);
-  __syncthreads();
-  if (wave == 0) {
-    add(slot_a);
-    put(slot_a);
-  }
-  __syncthreads();
-
-  const int64_t region = ((tslice * gridDim.x + strip) * splits) * kElems;
-  for (int e = tid; e < kElems; e += kThreads) {
-    const int tok = e / kStripRows;
-    const int nl = e - tok * kStripRows;
-    const float val = slot_a[tok * kRedStride + nl];
-    const int64_t n = n0 + nl;
-    if (tok >= m_rows || n >= N) continue;
-    if (splits == 1) {
-      out[(m_base + tok) * ldo + n] = OutCvt<OutT>::cvt(val);
-    } else {
-      // Agent-scope relaxed atomic stores write through to the device coherence point, so
-      // no L2 write-back fence is needed before the arrival counter is bumped.
-      __hip_atomic_store(&partials[region + split * kElems + e], val, __ATOMIC_RELAXED,
-                         __HIP_MEMORY_SCOPE_AGENT);
+          for (int v = 0; v < 4; ++v) acc[i][j][v] = __builtin_fmaf(p[v], sc, acc[i][j][v]);
+        }
     }
   }
-  if (splits == 1) return;
 
-  // Split-K: every partial store of this workgroup has completed (the barrier waits for
-  // outstanding memory operations) before one thread bumps the strip's counter; the
-  // workgroup that brings the count to `splits` sums the partials in split order.
+  // Lane holds D[n = 16 i + 4 g + v][token = 16 j + r]; stage as red[wave][token][n].
+  float* mine = red + wave * kTok * kStride;
+#pragma unroll
+  for (int i = 0; i < AF; ++i)
+#pragma unroll
+    for (int j = 0; j < NT; ++j)
+      *reinterpret_cast<float4*>(mine + (16 * j + r) * kStride + 16 * i + 4 * g) =
+          make_float4(acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]);
   __syncthreads();
-  if (tid == 0) {
-    const unsigned prev = __hip_atomic_fetch_add(&counters[tslice * gridDim.x + strip], 1u, __ATOMIC_RELAXED,
-                                                 __HIP_MEMORY_SCOPE_AGENT);
-    is_last = prev == static_cast<unsigned>(splits - 1);
-  }
-  __syncthreads();
-  if (!is_last) return;
-  for (int e = tid; e < kElems; e += kThreads) {
-    const int tok = e / kStripRows;
-    const int nl = e - tok * kStripRows;
+  for (int e = tid; e < kTok * kRows; e += kStreamWaves * 64) {
+    const int tok = e / kRows;
+    const int nl = e - tok * kRows;
     const int64_t n = n0 + nl;
     if (tok >= m_rows || n >= N) continue;
-    float val = 0.0f;
-    for (int64_t s = 0; s < splits; ++s)
-      val += __hip_atomic_load(&partials[region + s * kElems + e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    float val = red[tok * kStride + nl];
+#pragma unroll
+    for (int x = 1; x < kStreamWaves; ++x) val += red[x * kTok * kStride + tok * kStride + nl];
     out[(m_base + tok) * ldo + n] = OutCvt<OutT>::cvt(val);
   }
-  if (tid == 0)
-    __hip_atomic_store(&counters[tslice * gridDim.x + strip], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ------------------------------------------------------------------------------------
@@ -325,50 +279,44 @@ int plan_gemm(int64_t M, int64_t N, int64_t K, int config, GemmPlan* plan) {
   if (M < 0 || N < 0 || K <= 0) return MI355X_FP8_ERR_INVALID;
   *plan = GemmPlan{};
   if (config == MI355X_FP8_CONFIG_AUTO) config = M <= 64 ? MI355X_FP8_CONFIG_STREAM : MI355X_FP8_CONFIG_TILE128;
-  if (config != MI355X_FP8_CONFIG_STREAM && config != MI355X_FP8_CONFIG_TILE128) return MI355X_FP8_ERR_INVALID;
+  if (config != MI355X_FP8_CONFIG_STREAM && config != MI355X_FP8_CONFIG_TILE128 &&
+      config != MI355X_FP8_CONFIG_TILE256)
+    return MI355X_FP8_ERR_INVALID;
   plan->kernel = config;
-  if (config == MI355X_FP8_CONFIG_TILE128) return MI355X_FP8_OK;
-  const int64_t KB = cdiv(K, kGroup);
+  if (config != MI355X_FP8_CONFIG_STREAM) return MI355X_FP8_OK;
   const int64_t slice_rows = M < 64 ? M : 64;
   plan->token_tiles = slice_rows <= 16 ? 1 : (slice_rows <= 32 ? 2 : 4);
-  plan->strips = cdiv(N, kStripRows);
-  const int64_t slices = M > 0 ? cdiv(M, 64) : 0;
-  // The K split depends on K alone, never on M or N: a row's (or a column's) result is then
-  // the same whichever other rows or N-concatenated projections share the launch.
-  const int64_t kbps = KB <= 48 ? 4 : 8;  // one or two K groups per wave
-  plan->kb_per_split = kbps;
-  plan->splits = cdiv(KB, kbps);
-  if (plan->splits > 1) {
-    plan->partial_bytes = static_cast<size_t>(slices * plan->strips * plan->splits) *
-                          static_cast<size_t>(16 * plan->token_tiles * kStripRows) * sizeof(float);
-    if (slices * plan->strips > kCounterSlots) return MI355X_FP8_ERR_UNSUPPORTED;
-  }
+  // Two 16-row MFMA tiles per workgroup when N is wide enough to keep every CU busy
+  // anyway: halves the L2 re-reads of the activations.
+  plan->row_tiles = (plan->token_tiles <= 2 && N >= 16384) ? 2 : 1;
   return MI355X_FP8_OK;
 }
 
-size_t gemm_workspace_bytes(const GemmPlan& plan) {
-  // The counter region is reserved whatever the plan, so that it stays zero whichever
-  // sequence of shapes shares the workspace.
-  return kCounterRegionBytes + align256(plan.partial_bytes);
+size_t gemm_workspace_bytes(const GemmPlan&) { return 0; }
+
+template <int NT, int AF, bool ALIGNED, typename OutT>
+static void launch_stream_t(const uint8_t* q, int64_t ldq, const float* as, int64_t as_sm, int64_t as_sk,
+                            const uint8_t* w, int64_t ldw, const float* ws, int64_t ws_sn, int64_t ws_sk,
+                            uint16_t* out, int64_t ldo, int64_t M, int64_t N, int64_t K, hipStream_t stream) {
+  dim3 grid(static_cast<unsigned>(cdiv(N, 16 * AF)), 1, static_cast<unsigned>(cdiv(M, 64)));
+  stream_gemm_kernel<NT, AF, ALIGNED, OutT><<<grid, kStreamWaves * 64, 0, stream>>>(
+      q, ldq, as, as_sm, as_sk, w, ldw, ws, ws_sn, ws_sk, out, ldo, M, N, K, cdiv(K, kGroup));
 }
 
 template <bool ALIGNED, typename OutT>
 static void launch_stream(const GemmPlan& p, const uint8_t* q, int64_t ldq, const float* as,
                           int64_t as_sm, int64_t as_sk, const uint8_t* w, int64_t ldw,
                           const float* ws, int64_t ws_sn, int64_t ws_sk, uint16_t* out, int64_t ldo,
-                          int64_t M, int64_t N, int64_t K, float* partials, unsigned* counters,
-                          hipStream_t stream) {
-  const int64_t KB = cdiv(K, kGroup);
-  dim3 grid(static_cast<unsigned>(p.strips), static_cast<unsigned>(p.splits),
-            static_cast<unsigned>(cdiv(M, 64)));
-#define MI355X_STREAM_ARGS                                                                        \
-  q, ldq, as, as_sm, as_sk, w, ldw, ws, ws_sn, ws_sk, out, ldo, M, N, K, KB, p.kb_per_split,     \
-      p.splits, partials, counters
-  switch (p.token_tiles) {
-    case 1: stream_gemm_kernel<1, ALIGNED, OutT><<<grid, kThreads, 0, stream>>>(MI355X_STREAM_ARGS); break;
-    case 2: stream_gemm_kernel<2, ALIGNED, OutT><<<grid, kThreads, 0, stream>>>(MI355X_STREAM_ARGS); break;
-    default: stream_gemm_kernel<4, ALIGNED, OutT><<<grid, kThreads, 0, stream>>>(MI355X_STREAM_ARGS); break;
-  }
+                          int64_t M, int64_t N, int64_t K, hipStream_t stream) {
+#define MI355X_STREAM_ARGS q, ldq, as, as_sm, as_sk, w, ldw, ws, ws_sn, ws_sk, out, ldo, M, N, K, stream
+  if (p.token_tiles == 1)
+    p.row_tiles == 2 ? launch_stream_t<1, 2, ALIGNED, OutT>(MI355X_STREAM_ARGS)
+                     : launch_stream_t<1, 1, ALIGNED, OutT>(MI355X_STREAM_ARGS);
+  else if (p.token_tiles == 2)
+    p.row_tiles == 2 ? launch_stream_t<2, 2, ALIGNED, OutT>(MI355X_STREAM_ARGS)
+                     : launch_stream_t<2, 1, ALIGNED, OutT>(MI355X_STREAM_ARGS);
+  else
+    launch_stream_t<4, 1, ALIGNED, OutT>(MI355X_STREAM_ARGS);
 #undef MI355X_STREAM_ARGS
 }
 
@@ -389,11 +337,9 @@ static int launch_typed(const GemmPlan& plan, const uint8_t* q, int64_t ldq, con
                         int64_t ws_sn, int64_t ws_sk, uint16_t* out, int64_t ldo, int64_t M, int64_t N,
                         int64_t K, void* workspace, hipStream_t stream) {
   if (plan.kernel == MI355X_FP8_CONFIG_STREAM) {
-    if (plan.strips > 0x7fffffffLL || plan.splits > 65535 || cdiv(M, 64) > 65535) return MI355X_FP8_ERR_UNSUPPORTED;
-    unsigned* counters = static_cast<unsigned*>(workspace);
-    float* partials = reinterpret_cast<float*>(static_cast<char*>(workspace) + kCounterRegionBytes);
+    if (cdiv(N, 16) > 0x7fffffffLL || cdiv(M, 64) > 65535) return MI355X_FP8_ERR_UNSUPPORTED;
     launch_stream<ALIGNED, OutT>(plan, q, ldq, as, as_sm, as_sk, w, ldw, ws, ws_sn, ws_sk, out, ldo, M, N, K,
-                                 partials, counters, stream);
+                                 stream);
   } else {
     const int64_t tiles_m = cdiv(M, kTileM), tiles_n = cdiv(N, kTileN);
     if (tiles_m * tiles_n > 0x7fffffffLL) return MI355X_FP8_ERR_UNSUPPORTED;
@@ -409,6 +355,20 @@ int launch_block_gemm(const GemmPlan& plan, const uint8_t* q, int64_t ldq, const
                       int64_t ws_sn, int64_t ws_sk, void* out, int out_dtype, int64_t ldo,
                       int64_t M, int64_t N, int64_t K, void* workspace, hipStream_t stream) {
   if (M == 0 || N == 0) return MI355X_FP8_OK;
+  const bool dma_ok = tile_dma_supported(q, ldq, as_sm, as_sk, w, ldw, M, K);
+  if (plan.kernel == MI355X_FP8_CONFIG_TILE256) {
+    if (!dma_ok) return MI355X_FP8_ERR_UNSUPPORTED;
+    return launch_tile256(q, ldq, as, as_sk, w, ldw, ws, ws_sn, ws_sk, out, out_dtype, ldo, M, N, K, stream);
+  }
+  if (plan.kernel == MI355X_FP8_CONFIG_TILE128 && dma_ok) {
+    // 256x256 tiles halve the L2 traffic per flop but leave CUs idle when there are few
+    // of them; below about 160 tiles (o_proj and down at M=2048: 80) the 128x128 kernel,
+    // two workgroups per CU, finishes first.
+    const int64_t tiles256 = cdiv(M, 256) * cdiv(N, 256);
+    if (tiles256 >= 160)
+      return launch_tile256(q, ldq, as, as_sk, w, ldw, ws, ws_sn, ws_sk, out, out_dtype, ldo, M, N, K, stream);
+    return launch_tile_dma(q, ldq, as, as_sk, w, ldw, ws, ws_sn, ws_sk, out, out_dtype, ldo, M, N, K, stream);
+  }
   const bool aligned = (K % 16) == 0 && (ldq % 16) == 0 && (ldw % 16) == 0 &&
                        (reinterpret_cast<uintptr_t>(q) % 16) == 0 &&
                        (reinterpret_cast<uintptr_t>(w) % 16) == 0;

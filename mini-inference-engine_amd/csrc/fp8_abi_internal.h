@@ -13,31 +13,34 @@ int launch_act_quant(const void* x, int x_dtype, int64_t M, int64_t K, int64_t s
                      uint8_t* q, int64_t ldq, int64_t kpad, float* s, int64_t ssm, int64_t ssk,
                      hipStream_t stream);
 
-// Plan of one block-GEMM launch: which kernel, its grid, and the workspace it needs.
+// Plan of one block-GEMM launch: which kernel and its tile shape.
 struct GemmPlan {
-  int kernel;        // MI355X_FP8_CONFIG_STREAM or MI355X_FP8_CONFIG_TILE128
-  int token_tiles;   // stream kernel: 16-token MFMA tiles per wave (1, 2 or 4)
-  int64_t strips;    // stream kernel: 64-row strips of W
-  int64_t splits;    // stream kernel: K splits (workgroups per strip)
-  int64_t kb_per_split;
-  size_t partial_bytes;  // fp32 split-K partials
+  int kernel;       // MI355X_FP8_CONFIG_STREAM or MI355X_FP8_CONFIG_TILE128
+  int token_tiles;  // stream kernel: 16-token MFMA tiles per slice (1, 2 or 4)
+  int row_tiles;    // stream kernel: 16-row MFMA tiles of W per workgroup (1 or 2)
 };
-
-// Every workspace starts with a fixed region of per-strip arrival counters.  The caller
-// zero-fills it once; the stream kernel's last-arriving workgroup of each strip resets its
-// counter, so the region is zero again after every call, whatever shapes share it.
-constexpr int64_t kCounterSlots = 65536;
-constexpr size_t kCounterRegionBytes = kCounterSlots * sizeof(unsigned);
 
 int plan_gemm(int64_t M, int64_t N, int64_t K, int config, GemmPlan* plan);
 
-// Workspace layout: [counter region | partials], 256-byte aligned.
+// Device workspace the GEMM needs (none: every reduction stays inside a workgroup).
 size_t gemm_workspace_bytes(const GemmPlan& plan);
 
 int launch_block_gemm(const GemmPlan& plan, const uint8_t* q, int64_t ldq, const float* as,
                       int64_t as_sm, int64_t as_sk, const uint8_t* w, int64_t ldw, const float* ws,
                       int64_t ws_sn, int64_t ws_sk, void* out, int out_dtype, int64_t ldo,
                       int64_t M, int64_t N, int64_t K, void* workspace, hipStream_t stream);
+
+// LDS-DMA pipelined prefill kernel (tile_gemm_dma.hip) and its preconditions.
+bool tile_dma_supported(const uint8_t* q, int64_t ldq, int64_t as_sm, int64_t as_sk, const uint8_t* w,
+                        int64_t ldw, int64_t M, int64_t K);
+int launch_tile_dma(const uint8_t* q, int64_t ldq, const float* as, int64_t as_sk, const uint8_t* w,
+                    int64_t ldw, const float* ws, int64_t ws_sn, int64_t ws_sk, void* out, int out_dtype,
+                    int64_t ldo, int64_t M, int64_t N, int64_t K, hipStream_t stream);
+
+// 256x256-tile prefill kernel (tile_gemm_256.hip); same preconditions as the DMA kernel.
+int launch_tile256(const uint8_t* q, int64_t ldq, const float* as, int64_t as_sk, const uint8_t* w,
+                   int64_t ldw, const float* ws, int64_t ws_sn, int64_t ws_sk, void* out, int out_dtype,
+                   int64_t ldo, int64_t M, int64_t N, int64_t K, hipStream_t stream);
 
 inline size_t align256(size_t v) { return (v + 255) & ~static_cast<size_t>(255); }
 

@@ -26,6 +26,7 @@ DTYPE_F16 = 1
 CONFIG_AUTO = 0
 CONFIG_STREAM = 1
 CONFIG_TILE128 = 2
+CONFIG_TILE256 = 3
 OK = 0
 ERR_INVALID = 1
 ERR_UNSUPPORTED = 2

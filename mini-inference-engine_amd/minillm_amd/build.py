@@ -15,7 +15,7 @@ PACKAGE_DIR = os.path.dirname(os.path.abspath(__file__))
 CSRC_DIR = os.path.join(os.path.dirname(PACKAGE_DIR), "csrc")
 LIB_DIR = os.path.join(PACKAGE_DIR, "lib")
 LIB_PATH = os.path.join(LIB_DIR, "libmi355x_fp8.so")
-SOURCES = ("act_quant.hip", "block_gemm.hip", "abi.hip")
+SOURCES = ("act_quant.hip", "block_gemm.hip", "tile_gemm_dma.hip", "tile_gemm_256.hip", "abi.hip")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 FLAGS = (
@@ -24,6 +24,9 @@ FLAGS = (
     "-fno-fast-math",
     # No packed-fp32 VALU instructions (v_pk_*_f32) anywhere in the library.
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA results in ordinary VGPRs: the per-K-group fold (acc = fma(partial, scale, acc))
+    # then reads them directly instead of copying each element out of an AGPR first.
+    "-mllvm", "-amdgpu-mfma-vgpr-form=1",
 )
 
 

@@ -56,6 +56,7 @@ class FP8GemmConfig:
 GEMM_CONFIGS = (
     FP8GemmConfig("stream", _lib.CONFIG_STREAM, 64, 64),
     FP8GemmConfig("tile128", _lib.CONFIG_TILE128, 128, 128),
+    FP8GemmConfig("tile256", _lib.CONFIG_TILE256, 256, 256),
 )
 # Alias under the reference's name.
 SPLIT_GEMM_CONFIGS = GEMM_CONFIGS
@@ -122,11 +123,12 @@ def _dtype_code(dtype: torch.dtype) -> int:
 
 
 class _Workspace:
-    """Per (device, stream) zero-initialised byte buffer, grown on demand.
+    """Per (device, stream) scratch byte buffer, grown on demand.
 
-    The library leaves its split-K counters at zero after every call, so a buffer is
-    zero-filled only when it is (re)allocated.  Calls on one stream are ordered, so they
-    may share it; different streams get different buffers.
+    Calls on one stream are ordered, so they may share it; different streams get
+    different buffers.  Growing happens only on a larger shape than any seen before on
+    that stream (``pretune_mi355x_fp8`` warms the largest), so steady-state calls and
+    HIP-graph captures allocate nothing.
     """
 
     def __init__(self) -> None:
@@ -140,7 +142,7 @@ class _Workspace:
         buf = self._buffers.get(key)
         if buf is None or buf.numel() < nbytes:
             grown = max(nbytes, 0 if buf is None else 2 * buf.numel())
-            buf = torch.zeros(grown, dtype=torch.uint8, device=device)
+            buf = torch.empty(grown, dtype=torch.uint8, device=device)
             self._buffers[key] = buf
         return buf
 
@@ -155,15 +157,21 @@ def _stream_ptr(device: torch.device) -> int:
     return torch.cuda.current_stream(device).cuda_stream
 
 
-def quantize_mi355x_fp8_activation(input_2d: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+def quantize_mi355x_fp8_activation(input_2d: torch.Tensor, *, scale_layout: str = "row"
+                                   ) -> tuple[torch.Tensor, torch.Tensor]:
     """Quantize a 2-D activation once: ``(q [M, K] e4m3fn, s [M, ceil(K/128)] fp32)``.
 
     Same contract and errors as quantize_sm89_fp8_activation (sm89_fp8.py:401-424); the
-    input may have any strides, the outputs are contiguous and the scales raw.
+    input may have any strides, q is contiguous and the scales are raw.  With
+    ``scale_layout="kgroup"`` the scales are stored K-group-major (the returned ``s`` is a
+    strided [M, G] view of a [G, roundup(M, 64)] buffer, stride (1, roundup(M, 64))): the
+    layout the prefill GEMM streams into LDS.  Values are identical in both layouts.
     """
 
     if input_2d.ndim != 2 or input_2d.dtype not in {torch.bfloat16, torch.float16}:
         raise ValueError("Expected a 2D bf16/fp16 activation")
+    if scale_layout not in {"row", "kgroup"}:
+        raise ValueError(f"Unknown scale layout: {scale_layout!r}")
     if not input_2d.is_cuda or not mi355x_available(input_2d.device):
         raise RuntimeError("Activation quantization requires an MI355X (gfx950) GPU")
     m, k = input_2d.shape
@@ -171,11 +179,17 @@ def quantize_mi355x_fp8_activation(input_2d: torch.Tensor) -> tuple[torch.Tensor
         raise ValueError("Activation width must be positive")
     groups_k = (k + 127) // 128
     quantized = torch.empty((m, k), device=input_2d.device, dtype=torch.float8_e4m3fn)
-    scales = torch.empty((m, groups_k), device=input_2d.device, dtype=torch.float32)
+    if scale_layout == "row":
+        scales = torch.empty((m, groups_k), device=input_2d.device, dtype=torch.float32)
+        s_sm, s_sk = groups_k, 1
+    else:
+        mpad = max(64, -(-m // 64) * 64)
+        scales = torch.empty((groups_k, mpad), device=input_2d.device, dtype=torch.float32)[:, :m].t()
+        s_sm, s_sk = 1, mpad
     if m:
         _lib.check(_lib.load().mi355x_fp8_act_quant(
             input_2d.data_ptr(), _dtype_code(input_2d.dtype), m, k, input_2d.stride(0), input_2d.stride(1),
-            quantized.data_ptr(), k, k, scales.data_ptr(), groups_k, 1, _stream_ptr(input_2d.device)))
+            quantized.data_ptr(), k, k, scales.data_ptr(), s_sm, s_sk, _stream_ptr(input_2d.device)))
     return quantized, scales
 
 
