@@ -1,0 +1,87 @@
+"""The C-ABI library loads on a CPU-only machine and exports every symbol the header
+declares; argument validation and workspace sizing (host-only paths) behave as
+documented.  No call here reaches a kernel launch."""
+
+import ctypes
+import os
+import re
+
+import pytest
+
+from minillm_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "mi355x_fp8.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\w[\w\s\*]*?\b(mi355x_fp8_\w+)\s*\(", text, re.MULTILINE)))
+
+
+def test_header_declares_the_bound_entry_points():
+    assert declared_functions() == sorted(_lib.EXPORTS)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    for name in declared_functions():
+        assert getattr(lib, name) is not None
+    assert lib.mi355x_fp8_abi_version() == _lib.ABI_VERSION
+
+
+def test_header_constants_match_binding():
+    text = open(HEADER).read()
+    for macro, value in {"MI355X_FP8_DTYPE_BF16": _lib.DTYPE_BF16, "MI355X_FP8_DTYPE_F16": _lib.DTYPE_F16,
+                         "MI355X_FP8_CONFIG_AUTO": _lib.CONFIG_AUTO, "MI355X_FP8_CONFIG_STREAM": _lib.CONFIG_STREAM,
+                         "MI355X_FP8_CONFIG_TILE128": _lib.CONFIG_TILE128,
+                         "MI355X_FP8_CONFIG_TILE256": _lib.CONFIG_TILE256, "MI355X_FP8_OK": _lib.OK,
+                         "MI355X_FP8_ERR_INVALID": _lib.ERR_INVALID, "MI355X_FP8_ERR_UNSUPPORTED": _lib.ERR_UNSUPPORTED,
+                         "MI355X_FP8_ERR_WORKSPACE": _lib.ERR_WORKSPACE, "MI355X_FP8_ERR_LAUNCH": _lib.ERR_LAUNCH,
+                         "MI355X_FP8_ABI_VERSION": _lib.ABI_VERSION}.items():
+        assert re.search(rf"#define {macro} {value}\b", text), macro
+
+
+def test_status_strings_and_exception_mapping():
+    lib = _lib.load()
+    assert lib.mi355x_fp8_status_string(0) == b"ok"
+    assert b"workspace" in lib.mi355x_fp8_status_string(_lib.ERR_WORKSPACE)
+    with pytest.raises(ValueError):
+        _lib.check(_lib.ERR_INVALID)
+    with pytest.raises(ValueError):
+        _lib.check(_lib.ERR_WORKSPACE)
+    with pytest.raises(RuntimeError):
+        _lib.check(_lib.ERR_UNSUPPORTED)
+    _lib.check(_lib.OK)
+
+
+def test_workspace_sizes():
+    lib = _lib.load()
+    # The GEMM needs no workspace; the linear needs room for q (M x Kpad) and scales.
+    assert lib.mi355x_fp8_block_gemm_workspace_bytes(8, 6144, 2560, 0) == 0
+    need = lib.mi355x_fp8_linear_workspace_bytes(8, 6144, 2560, 0)
+    assert need >= 8 * 2560 + 4 * 20 * 8
+    assert lib.mi355x_fp8_linear_workspace_bytes(2048, 2560, 9728, 0) >= 2048 * 9728 + 4 * 76 * 2048
+    assert lib.mi355x_fp8_linear_workspace_bytes(8, 6144, 0, 0) == 0     # K == 0: invalid
+    assert lib.mi355x_fp8_linear_workspace_bytes(8, 6144, 2560, 99) == 0  # unknown config
+
+
+def test_argument_validation_happens_before_any_launch():
+    lib = _lib.load()
+    null = None
+    # Invalid dtype / K / kpad: rejected on the host.
+    assert lib.mi355x_fp8_act_quant(null, 7, 4, 128, 128, 1, null, 128, 128, null, 1, 1, null) == _lib.ERR_INVALID
+    assert lib.mi355x_fp8_act_quant(null, 0, 4, 0, 128, 1, null, 128, 128, null, 1, 1, null) == _lib.ERR_INVALID
+    assert lib.mi355x_fp8_act_quant(null, 0, 4, 128, 128, 1, null, 128, 64, null, 1, 1, null) == _lib.ERR_INVALID
+    # M == 0 is a no-op even with null pointers.
+    assert lib.mi355x_fp8_act_quant(null, 0, 0, 128, 128, 1, null, 128, 128, null, 1, 1, null) == _lib.OK
+    assert lib.mi355x_fp8_block_gemm(null, 128, null, 1, 1, null, 128, null, 1, 1, null, 0, 64, 0, 64, 128,
+                                     null, 0, 0, null) == _lib.OK
+    assert lib.mi355x_fp8_block_gemm(null, 64, null, 1, 1, null, 128, null, 1, 1, null, 0, 64, 4, 64, 128,
+                                     null, 0, 0, null) == _lib.ERR_INVALID   # ldq < K
+    assert lib.mi355x_fp8_block_gemm(null, 128, null, 1, 1, null, 128, null, 1, 1, null, 0, 64, 4, 64, 128,
+                                     null, 0, 9, null) == _lib.ERR_INVALID   # unknown config
+    # The linear refuses a missing workspace before launching anything.
+    dummy = ctypes.c_void_p(16)
+    assert lib.mi355x_fp8_linear(dummy, 0, 4, 128, 128, 1, dummy, 128, dummy, 1, 1, 64, dummy, 0, 64, null, 0, 0,
+                                 null) == _lib.ERR_WORKSPACE
