@@ -38,10 +38,17 @@ constexpr int kThreads = 256;  // tile kernel
 // One workgroup owns 16*AF consecutive W rows and reads them over the whole of K exactly
 // once.  Its WAVES waves take K groups round-robin (wave w: w, w + WAVES, ...), each
 // keeping D groups of loads in flight, and combine their fp32 partials through LDS in
-// wave order.  The assignment of K groups to waves depends on K alone, so a row's result
+// wave order.  16 waves with one group in flight each measured best on the Qwen3-4B
+// shapes (8 or 4 waves with 2-4 groups in flight were 5-20 % slower).  The assignment of K groups to waves depends on K alone, so a row's result
 // is the same whatever M is or whichever projections are concatenated along N.
-constexpr int kStreamWaves = 8;
-constexpr int kStreamDepth = 2;
+#ifndef MI355X_STREAM_WAVES
+#define MI355X_STREAM_WAVES 16
+#endif
+#ifndef MI355X_STREAM_DEPTH
+#define MI355X_STREAM_DEPTH 1
+#endif
+constexpr int kStreamWaves = MI355X_STREAM_WAVES;
+constexpr int kStreamDepth = MI355X_STREAM_DEPTH;
 
 template <int NT, int AF, bool ALIGNED, typename OutT>
 __global__ __launch_bounds__(kStreamWaves * 64) void stream_gemm_kernel(

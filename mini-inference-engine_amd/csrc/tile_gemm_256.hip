@@ -36,21 +36,39 @@ namespace {
 constexpr int kT256Threads = 512;
 constexpr int kRowsT = 256;
 constexpr int kTileChunks = kRowsT * 8;                 // one 256 x 128 B tile, in uint4
-constexpr int kScaleOff = 2 * kTileChunks;              // 8 waves x 64 floats
-constexpr int kStageU4 = 2 * kTileChunks + 128;
-constexpr int kDmaPerStage256 = 9;
+constexpr int kSinkOff = 2 * kTileChunks;              // 8 waves x 256 B written by the L2 prefetch, never read
+constexpr int kStageU4 = kSinkOff + 128;
+
 
 __shared__ uint4 t256_stage0[kStageU4];
 __shared__ uint4 t256_stage1[kStageU4];
 
-typedef __attribute__((address_space(3))) void lds_void_t;
-typedef const __attribute__((address_space(1))) void global_void_t;
+// K groups ahead of the one being multiplied that each step pulls into L2 (0: none).
+// Off by default: on the Qwen3-4B shapes every distance tried (2, 4, 8) was slower than
+// none (the extra 4-byte DMA per lane costs more than the L2 hits it buys).
+#ifndef MI355X_T256_PREFETCH
+#define MI355X_T256_PREFETCH 0
+#endif
+constexpr int kPrefetchAhead = MI355X_T256_PREFETCH;
 
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+// The DMA instructions are issued through inline assembly.  The compiler then does not
+// track them, so it adds no waits of its own before LDS reads of the *other* stage (its
+// alias tracking of LDS DMA is not precise enough for this kernel and would serialise every
+// step on the DMA latency).  Every wait for them is explicit: the vmcnt waits before the
+// workgroup barriers.  (Untracked loads can only make the compiler's own vmcnt waits for
+// ordinary loads stricter, never looser.)  M0 is written without being declared clobbered
+// (it is a reserved register): nothing else in this kernel uses M0, as every LDS DMA of it
+// goes through these two helpers.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_void_t*)(p)));
+}
 __device__ __forceinline__ void dma16(const void* src, void* lds_dst) {
-  __builtin_amdgcn_global_load_lds((global_void_t*)(src), (lds_void_t*)(lds_dst), 16, 0, 0);
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds_addr(lds_dst)) : "memory");
 }
 __device__ __forceinline__ void dma4(const void* src, void* lds_dst) {
-  __builtin_amdgcn_global_load_lds((global_void_t*)(src), (lds_void_t*)(lds_dst), 4, 0, 0);
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off" ::"v"(src), "s"(lds_addr(lds_dst)) : "memory");
 }
 
 template <int S>
@@ -62,11 +80,15 @@ __device__ __forceinline__ uint4* stage256() {
 struct Src256 {
   const uint8_t* w[4];
   const uint8_t* x[4];
-  const float* as;
+  const float* as;   // activation scales of K group 0
+  int as_row[4];     // this lane's rows 64 wm + 16 j + r, clamped to M - 1
+  const uint8_t* pf;  // this thread's 128-byte line of the tile (W rows, then X rows)
 };
 
+// Fills stage S with K group kb and pulls K group kp's tile lines into L2 (the 4-byte
+// prefetch lands in the stage's sink, so every DMA of a step targets one LDS object).
 template <int S>
-__device__ __forceinline__ void issue256(const Src256& src, int64_t kb, int64_t as_sk, int wave) {
+__device__ __forceinline__ void issue256(const Src256& src, int64_t kb, int64_t kp, int64_t as_sk, int wave) {
   uint4* st = stage256<S>();
   const int64_t koff = kb * kGroup;
 #pragma unroll
@@ -74,7 +96,7 @@ __device__ __forceinline__ void issue256(const Src256& src, int64_t kb, int64_t 
     dma16(src.w[i] + koff, st + (i * 8 + wave) * 64);
     dma16(src.x[i] + koff, st + kTileChunks + (i * 8 + wave) * 64);
   }
-  dma4(src.as + kb * as_sk, reinterpret_cast<float*>(st + kScaleOff) + wave * 64);
+  if constexpr (kPrefetchAhead > 0) dma4(src.pf + kp * kGroup, reinterpret_cast<float*>(st + kSinkOff) + wave * 64);
 }
 
 template <int S>
@@ -88,15 +110,15 @@ __device__ __forceinline__ v8i frag(const uint4* tile, int row, int g) {
 // LDS latency of a fragment hides behind 8 x 32 MFMA cycles and the registers left over
 // (accumulators take 128) let several MFMA results be in flight before they are folded.
 template <int S>
-__device__ __forceinline__ void compute256(v4f (&acc)[8][4], float wsv, int wm, int wn, int r, int g) {
+__device__ __forceinline__ void compute256(v4f (&acc)[8][4], const float (&asv)[4], float wsv, int wm, int wn,
+                                           int r, int g) {
   const uint4* st = stage256<S>();
-  const float* sc_lds = reinterpret_cast<const float*>(st + kScaleOff) + wm * 64;  // rows 64 wm ..
   v8i b[4];
   float sc[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     b[j] = frag<S>(st + kTileChunks, wm * 64 + 16 * j + r, g);
-    sc[j] = sc_lds[16 * j + r] * wsv;
+    sc[j] = asv[j] * wsv;
   }
   v8i a0 = frag<S>(st, wn * 128 + r, g);
   v8i a1 = frag<S>(st, wn * 128 + 16 + r, g);
@@ -116,13 +138,39 @@ __device__ __forceinline__ void compute256(v4f (&acc)[8][4], float wsv, int wm, 
   }
 }
 
+// One K group.  Per wave and step the memory instructions are, in order: the 9 DMA loads
+// of the next K group into the other stage, then one 4-byte DMA per lane that touches
+// the K group kPrefetchAhead steps ahead (one 128-byte line per thread, 512 lines = the
+// whole W and activation tile), so that its later DMA finds the data in L2 instead of
+// paying the HBM latency with only one stage of lookahead.  Waiting for the current
+// stage therefore leaves exactly the newest prefetch outstanding: vmcnt(1).
+// Wait until this wave's DMA of the next stage has landed (everything but the newest
+// prefetch: vmcnt(1)) and every wave has done the same and finished reading the current
+// stage.  The wait sits at the end of a step, not the start, so that the loop's back edge
+// follows it directly (the compiler then needs no wait of its own before the reads).
+__device__ __forceinline__ void sync_stage() {
+  __builtin_amdgcn_s_waitcnt(0x70 | (kPrefetchAhead > 0 ? 1 : 0));  // vmcnt(1 or 0), lgkmcnt(0)
+  __builtin_amdgcn_s_barrier();
+}
+
 template <int CUR>
-__device__ __forceinline__ void step256(v4f (&acc)[8][4], const Src256& src, int64_t kb, int64_t KB, int64_t as_sk,
-                                        const float* ws_row, int64_t ws_sk, int wave, int wm, int wn, int r, int g) {
-  __builtin_amdgcn_s_waitcnt(0x70);  // vmcnt(0), lgkmcnt(0): this wave's DMA of stage CUR landed
-  __builtin_amdgcn_s_barrier();      // ... and every other wave's; stage CUR^1 is free
-  issue256<CUR ^ 1>(src, kb + 1 < KB ? kb + 1 : KB - 1, as_sk, wave);
-  if (kb < KB) compute256<CUR>(acc, ws_row[kb * ws_sk], wm, wn, r, g);
+__device__ __forceinline__ void step256(v4f (&acc)[8][4], const float (&asv)[4], float (&next)[4], const Src256& src,
+                                        int64_t kb, int64_t KB,
+                                        int64_t as_sk, const float* ws_row, int64_t ws_sk, int wave, int wm, int wn,
+                                        int r, int g) {
+  // The activation scales of K group kb + 1 go to registers (plain loads, L2 hits), issued
+  // before the DMA batch so that the end-of-step vmcnt(1) also covers them; the two
+  // unrolled steps alternate between two register sets, so no copy waits for a load.
+  const int64_t kn = kb + 1 < KB ? kb + 1 : KB - 1;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) next[j] = src.as[kn * as_sk + src.as_row[j]];
+  // Keep the issue order scales, DMA batch, prefetch (compiler and scheduler barriers).
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+  issue256<CUR ^ 1>(src, kn, kb + kPrefetchAhead < KB ? kb + kPrefetchAhead : KB - 1, as_sk, wave);
+  __builtin_amdgcn_sched_barrier(0);
+  compute256<CUR>(acc, asv, ws_row[kb * ws_sk], wm, wn, r, g);
+  sync_stage();
 }
 
 __device__ __forceinline__ void tile_order(int64_t pid, int64_t tiles_m, int64_t tiles_n, int64_t* tm, int64_t* tn) {
@@ -142,6 +190,12 @@ __device__ __forceinline__ void tile_order(int64_t pid, int64_t tiles_m, int64_t
   *tn = within / gm;
 }
 
+#ifdef MI355X_T256_TIMING
+// Development instrumentation only (never compiled into the library): per-workgroup
+// start/end timestamps (s_memrealtime, 100 MHz) and the hardware id of the CU.
+__device__ unsigned long long t256_timing[1 << 16][3];
+#endif
+
 template <typename OutT>
 __global__ __launch_bounds__(kT256Threads, 2) void tile256_gemm_kernel(
     const uint8_t* __restrict__ q, int64_t ldq, const float* __restrict__ as, int64_t as_sk,
@@ -149,6 +203,9 @@ __global__ __launch_bounds__(kT256Threads, 2) void tile256_gemm_kernel(
     int64_t ws_sk, uint16_t* __restrict__ out, int64_t ldo, int64_t M, int64_t N, int64_t KB,
     int64_t tiles_m, int64_t tiles_n, int vec_out) {
   const int tid = threadIdx.x;
+#ifdef MI355X_T256_TIMING
+  const unsigned long long t_start = __builtin_amdgcn_s_memrealtime();
+#endif
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63;
   const int r = lane & 15;
@@ -171,8 +228,14 @@ __global__ __launch_bounds__(kT256Threads, 2) void tile256_gemm_kernel(
     src.x[i] = q + xrow * ldq + 16 * c;
   }
   {
-    const int64_t srow = m0 + (wave & 3) * 64 + lane;  // waves 4..7 duplicate 0..3
-    src.as = as + (srow < M ? srow : M - 1);
+    src.as = as;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int64_t row = m0 + wm * 64 + 16 * j + r;
+      src.as_row[j] = static_cast<int>(row < M ? row : M - 1);
+    }
+    const int64_t prow = tid < kRowsT ? n0 + tid : m0 + tid - kRowsT;
+    src.pf = tid < kRowsT ? w + (prow < N ? prow : N - 1) * ldw : q + (prow < M ? prow : M - 1) * ldq;
   }
   const int64_t nw = n0 + wn * 128;
   const float* ws_row = ws + ((nw < N ? nw : N - 1) / kGroup) * ws_sn;
@@ -183,11 +246,20 @@ __global__ __launch_bounds__(kT256Threads, 2) void tile256_gemm_kernel(
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
 
-  issue256<0>(src, 0, as_sk, wave);
-  for (int64_t kb = 0; kb < KB; kb += 2) {
-    step256<0>(acc, src, kb, KB, as_sk, ws_row, ws_sk, wave, wm, wn, r, g);
-    step256<1>(acc, src, kb + 1, KB, as_sk, ws_row, ws_sk, wave, wm, wn, r, g);
+  float as_even[4], as_odd[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) as_even[j] = src.as[src.as_row[j]];
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+  issue256<0>(src, 0, KB > kPrefetchAhead - 1 ? kPrefetchAhead - 1 : KB - 1, as_sk, wave);
+  __builtin_amdgcn_sched_barrier(0);
+  sync_stage();
+  int64_t kb = 0;
+  for (; kb + 1 < KB; kb += 2) {
+    step256<0>(acc, as_even, as_odd, src, kb, KB, as_sk, ws_row, ws_sk, wave, wm, wn, r, g);
+    step256<1>(acc, as_odd, as_even, src, kb + 1, KB, as_sk, ws_row, ws_sk, wave, wm, wn, r, g);
   }
+  if (kb < KB) step256<0>(acc, as_even, as_odd, src, kb, KB, as_sk, ws_row, ws_sk, wave, wm, wn, r, g);
   __builtin_amdgcn_s_waitcnt(0x70);  // no DMA may still target LDS when the workgroup ends
 
   // Lane holds out[m = m0 + 64 wm + 16 j + r][n = n0 + 128 wn + 16 i + 4 g + v].
@@ -212,6 +284,14 @@ __global__ __launch_bounds__(kT256Threads, 2) void tile256_gemm_kernel(
       }
     }
   }
+#ifdef MI355X_T256_TIMING
+  __syncthreads();
+  if (tid == 0 && blockIdx.x < (1u << 16)) {
+    t256_timing[blockIdx.x][0] = t_start;
+    t256_timing[blockIdx.x][1] = __builtin_amdgcn_s_memrealtime();
+    t256_timing[blockIdx.x][2] = __builtin_amdgcn_s_getreg((4 << 0) | (0 << 6) | (31 << 11));  // HW_ID
+  }
+#endif
 }
 
 }  // namespace
