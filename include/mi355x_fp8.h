@@ -98,6 +98,21 @@ int mi355x_fp8_linear(const void* x, int x_dtype, int64_t M, int64_t K, int64_t 
                       int64_t ldo, void* workspace, size_t workspace_bytes, int config,
                       void* stream);
 
+/*
+ * Fused SiLU(gate) * up followed by the activation quantizer, for the MLP's down_proj.
+ * Replaces silu_mul (engine/kernels/fused.py:127-137, 217-232) plus the quantizer launch of
+ * the down projection (engine/kernels/sm89_fp8.py:401-424) in _mlp_forward
+ * (fused.py:280-283).
+ *   gate, up : M x I bf16, (m, i) at gate[m*ld + i] / up[m*ld + i] (for one merged
+ *              gate_up output: up = gate + I, ld = 2 I)
+ *   h        : optional (NULL: not written) bf16 bf16(bf16(silu(g)) * u), (m, i) at h[m*ldh + i]
+ *   q, s     : quantized h and its raw fp32 scales, as in mi355x_fp8_act_quant
+ * x_dtype must be MI355X_FP8_DTYPE_BF16 (fp16 returns MI355X_FP8_ERR_UNSUPPORTED).
+ */
+int mi355x_fp8_silu_mul_quant(const void* gate, const void* up, int x_dtype, int64_t M, int64_t I,
+                              int64_t ld, void* h, int64_t ldh, uint8_t* q, int64_t ldq, int64_t kpad,
+                              float* s, int64_t s_sm, int64_t s_sk, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

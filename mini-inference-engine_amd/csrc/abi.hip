@@ -58,6 +58,18 @@ int mi355x_fp8_act_quant(const void* x, int x_dtype, int64_t M, int64_t K, int64
                           static_cast<hipStream_t>(stream));
 }
 
+int mi355x_fp8_silu_mul_quant(const void* gate, const void* up, int x_dtype, int64_t M, int64_t I,
+                              int64_t ld, void* h, int64_t ldh, uint8_t* q, int64_t ldq, int64_t kpad,
+                              float* s, int64_t s_sm, int64_t s_sk, void* stream) {
+  if (!valid_dtype(x_dtype) || M < 0 || I <= 0 || ld < I || kpad < I || kpad > cdiv64(I, 128) * 128 ||
+      ldq < kpad || (h != nullptr && ldh < I))
+    return MI355X_FP8_ERR_INVALID;
+  if (M == 0) return MI355X_FP8_OK;
+  if (!gate || !up || !q || !s) return MI355X_FP8_ERR_INVALID;
+  return launch_silu_mul_quant(gate, up, x_dtype, ld, M, I, static_cast<uint16_t*>(h), ldh, q, ldq, kpad, s, s_sm,
+                               s_sk, static_cast<hipStream_t>(stream));
+}
+
 size_t mi355x_fp8_block_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int config) {
   GemmPlan plan;
   if (plan_gemm(M, N, K, config, &plan) != MI355X_FP8_OK) return 0;

@@ -13,6 +13,10 @@ int launch_act_quant(const void* x, int x_dtype, int64_t M, int64_t K, int64_t s
                      uint8_t* q, int64_t ldq, int64_t kpad, float* s, int64_t ssm, int64_t ssk,
                      hipStream_t stream);
 
+int launch_silu_mul_quant(const void* gate, const void* up, int dtype, int64_t ld, int64_t M, int64_t I,
+                          uint16_t* h_out, int64_t ldh, uint8_t* q, int64_t ldq, int64_t kpad, float* s,
+                          int64_t ssm, int64_t ssk, hipStream_t stream);
+
 // Plan of one block-GEMM launch: which kernel and its tile shape.
 struct GemmPlan {
   int kernel;       // MI355X_FP8_CONFIG_STREAM or MI355X_FP8_CONFIG_TILE128

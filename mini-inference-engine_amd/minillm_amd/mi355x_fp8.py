@@ -361,3 +361,73 @@ def uninstall_mi355x_fp8_dispatch() -> None:
 
     finegrained_fp8.fp8_linear = _original_fp8_linear
     _original_fp8_linear = None
+
+
+def silu_mul_quant_mi355x_fp8(gate: torch.Tensor, up: torch.Tensor, *, scale_layout: str = "kgroup",
+                              return_intermediate: bool = False):
+    """``SiLU(gate) * up`` in bf16, quantized per row and 128-column group, in one kernel.
+
+    The elementwise part is the reference's silu_mul (engine/kernels/fused.py:127-137,
+    217-232: silu rounded to bf16, then a bf16 multiply); the quantization is the
+    activation quantizer's (sm89_fp8.py:304-332).  ``gate`` and ``up`` are [..., I] bf16
+    with the same row stride and unit column stride (e.g. the two column views of one
+    merged gate_up output).  Returns ``(q, s)`` or, with ``return_intermediate``,
+    ``(h, q, s)`` where h is the bf16 product (what the reference feeds to down_proj).
+    """
+
+    if gate.shape != up.shape or gate.dtype != torch.bfloat16 or up.dtype != torch.bfloat16:
+        raise ValueError("gate and up must be bf16 tensors of one shape")
+    if scale_layout not in {"row", "kgroup"}:
+        raise ValueError(f"Unknown scale layout: {scale_layout!r}")
+    if not gate.is_cuda or not mi355x_available(gate.device):
+        raise RuntimeError("silu_mul_quant requires an MI355X (gfx950) GPU")
+    i = int(gate.shape[-1])
+    if i == 0:
+        raise ValueError("Width must be positive")
+    g2, u2 = gate.reshape(-1, i), up.reshape(-1, i)
+    if g2.stride(-1) != 1 or u2.stride(-1) != 1 or g2.stride(0) != u2.stride(0):
+        g2, u2 = g2.contiguous(), u2.contiguous()
+    m = g2.shape[0]
+    groups = (i + 127) // 128
+    q = torch.empty((m, i), device=gate.device, dtype=torch.float8_e4m3fn)
+    if scale_layout == "row":
+        s = torch.empty((m, groups), device=gate.device, dtype=torch.float32)
+        s_sm, s_sk = groups, 1
+    else:
+        mpad = max(64, -(-m // 64) * 64)
+        s = torch.empty((groups, mpad), device=gate.device, dtype=torch.float32)[:, :m].t()
+        s_sm, s_sk = 1, mpad
+    h = torch.empty((m, i), device=gate.device, dtype=torch.bfloat16) if return_intermediate else None
+    if m:
+        _lib.check(_lib.load().mi355x_fp8_silu_mul_quant(
+            g2.data_ptr(), u2.data_ptr(), _lib.DTYPE_BF16, m, i, g2.stride(0),
+            None if h is None else h.data_ptr(), i, q.data_ptr(), i, i, s.data_ptr(), s_sm, s_sk,
+            _stream_ptr(gate.device)))
+    shape = tuple(gate.shape)
+    q = q.reshape(shape)
+    if h is not None:
+        return h.reshape(shape), q, s
+    return q, s
+
+
+def mlp_forward_mi355x_fp8(x: torch.Tensor, gate_up_weight: torch.Tensor, gate_up_scale: torch.Tensor,
+                           down_weight: torch.Tensor, down_scale: torch.Tensor,
+                           output_dtype: torch.dtype | None = None) -> torch.Tensor:
+    """Qwen3 MLP on FP8 weights: ``down(SiLU(gate) * up)`` with merged gate/up.
+
+    The reference's _mlp_forward (engine/kernels/fused.py:280-283) runs merged gate_up ->
+    silu_mul -> down_proj, quantizing the bf16 product again inside down_proj.  Here the
+    SiLU-mul writes the quantized product directly (one kernel instead of silu_mul plus the
+    down projection's quantizer); the codes are those the quantizer would give for the
+    same bf16 product.
+    """
+
+    k = int(x.shape[-1])
+    gate_up = mi355x_fp8_linear(x.reshape(-1, k), gate_up_weight, gate_up_scale, [128, 128])
+    inter = gate_up.shape[-1] // 2
+    q, s = silu_mul_quant_mi355x_fp8(gate_up[:, :inter], gate_up[:, inter:])
+    out = torch.empty((q.shape[0], down_weight.shape[0]), device=x.device, dtype=output_dtype or x.dtype)
+    if q.shape[0]:
+        launch_block_gemm(q, down_weight if down_weight.stride(-1) == 1 else down_weight.contiguous(), out, s,
+                          down_scale)
+    return out.reshape(*x.shape[:-1], down_weight.shape[0])

@@ -214,6 +214,23 @@ void orc_linear(const uint16_t* x, int is_fp16, int64_t M, int64_t K, int64_t sx
                  nthreads);
 }
 
+/* SiLU(gate) * up in bf16, following the reference's _silu_mul_kernel
+ * (engine/kernels/fused.py:127-137): silu = bf16(g / (1 + exp(-g))) in fp32 with an IEEE
+ * division, then bf16(silu * u).  exp(-g) is evaluated in binary64 and rounded once to
+ * binary32 (the correctly rounded fp32 exp in all but double-rounding corner cases); a GPU's
+ * faithfully rounded expf may differ in the last place, so callers compare h within one
+ * bf16 ulp and quantize the GPU's own h for the bit-exact code check. */
+void orc_silu_mul(const uint16_t* gate, const uint16_t* up, int64_t n, uint16_t* h) {
+  for (int64_t i = 0; i < n; ++i) {
+    float g = orc_bf16_to_f32(gate[i]);
+    float u = orc_bf16_to_f32(up[i]);
+    float e = (float)exp(-(double)g);
+    float den = 1.0f + e;
+    float silu = orc_bf16_to_f32(orc_f32_to_bf16(g / den));
+    h[i] = orc_f32_to_bf16(silu * u);
+  }
+}
+
 int orc_max_threads(void) {
 #ifdef _OPENMP
   return omp_get_max_threads();

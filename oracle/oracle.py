@@ -53,6 +53,7 @@ def lib():
             _ptr, ctypes.c_int, _i64, _i64, _i64, _i64, _ptr, _ptr, _i64, _ptr, ctypes.c_int,
             _ptr, _ptr, ctypes.c_int]
         handle.orc_max_threads.restype = ctypes.c_int
+        handle.orc_silu_mul.argtypes = [_ptr, _ptr, _i64, _ptr]
         _lib = handle
     return _lib
 
@@ -136,6 +137,18 @@ def f32_to_bf16_bits(x: np.ndarray) -> np.ndarray:
     x = np.ascontiguousarray(x, dtype=np.float32)
     f = np.vectorize(lambda v: lib().orc_f32_to_bf16(float(v)), otypes=[np.uint16])
     return f(x) if x.size else np.empty(x.shape, dtype=np.uint16)
+
+
+def silu_mul(gate_bits: np.ndarray, up_bits: np.ndarray) -> np.ndarray:
+    """bf16 SiLU(gate) * up (reference engine/kernels/fused.py:127-137), as bf16 bits."""
+
+    g = np.ascontiguousarray(gate_bits, dtype=np.uint16)
+    u = np.ascontiguousarray(up_bits, dtype=np.uint16)
+    if g.shape != u.shape:
+        raise ValueError("shape mismatch")
+    out = np.empty(g.shape, dtype=np.uint16)
+    lib().orc_silu_mul(_p(g), _p(u), g.size, _p(out))
+    return out
 
 
 def max_threads() -> int:

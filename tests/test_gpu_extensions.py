@@ -1,0 +1,112 @@
+"""GPU checks of the rows next to the linear: the fused SiLU-mul + requant kernel, the MLP
+block built on it (baseline config 4) and merged projections (bitwise equal to separate
+calls, as the reference's tests/test_merged_projections.py:42-56 requires)."""
+
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from _helpers import assert_close_rows, bits16, codes, oracle_linear
+from minillm_amd import merged_projections as mp
+from minillm_amd import mi355x_fp8 as fp8
+from minillm_amd.validation import (
+    SEED, ModelShape, bitwise_equal, make_activations, make_baseline_activations, make_baseline_weights,
+    make_weights,
+)
+
+pytestmark = pytest.mark.gpu
+
+
+def _note(*parts):
+    print("CASE", *parts, flush=True, file=sys.stderr)
+
+
+def _bf16(bits):
+    return torch.from_numpy(np.ascontiguousarray(bits).view(np.int16)).view(torch.bfloat16)
+
+
+@pytest.mark.parametrize("rows,inter", [(1, 9728), (7, 259), (64, 1024), (300, 9728)])
+def test_silu_mul_quant_matches_oracle(gpu, rows, inter):
+    """h within one bf16 ulp of the oracle (exp may differ in the last place), and the
+    codes/scales bit-exact against the oracle's quantizer applied to the kernel's own h."""
+
+    _note("silu_mul_quant", rows, inter)
+    gen = torch.Generator().manual_seed(rows * 7 + inter)
+    gate_up = (torch.randn(rows, 2 * inter, generator=gen) * 3).to(torch.bfloat16)
+    gate_up[0, :8] = torch.tensor([0.0, -0.0, 30.0, -30.0, 88.0, -100.0, 1e-3, 5.0]).to(torch.bfloat16)
+    g, u = gate_up[:, :inter], gate_up[:, inter:]
+    dev = gate_up.to(gpu)
+    h, q, s = fp8.silu_mul_quant_mi355x_fp8(dev[:, :inter], dev[:, inter:], scale_layout="row",
+                                           return_intermediate=True)
+    ref_h = oracle.silu_mul(bits16(g.contiguous()), bits16(u.contiguous()))
+    got_h = bits16(h)
+    ulps = np.abs(got_h.astype(np.int32) - ref_h.astype(np.int32))
+    assert ulps.max() <= 1 and (ulps == 0).mean() > 0.999
+    q_ref, s_ref = oracle.act_quant(got_h)
+    assert np.array_equal(codes(q), q_ref)
+    assert np.array_equal(s.cpu().numpy().view(np.uint32), s_ref.view(np.uint32))
+    # K-group-major scales: same values.
+    q2, s2 = fp8.silu_mul_quant_mi355x_fp8(dev[:, :inter], dev[:, inter:])
+    assert bitwise_equal(q2, q) and bitwise_equal(s2.contiguous(), s)
+
+
+def test_silu_mul_quant_rejects_fp16(gpu):
+    x = torch.zeros(2, 256, dtype=torch.float16, device=gpu)
+    with pytest.raises(ValueError, match="bf16"):
+        fp8.silu_mul_quant_mi355x_fp8(x, x)
+
+
+@pytest.mark.parametrize("rows", [8, 512])
+def test_mlp_block_config4(gpu, rows):
+    """Baseline config 4 at M in {8, 512}: x -> gate_up -> SiLU*up -> requant -> down, against
+    the oracle run on the same chain (its quantizer applied to the GPU's bf16 product)."""
+
+    _note("mlp", rows)
+    gu_shape, down_shape = ModelShape("gate_up", 19456, 2560), ModelShape("down", 2560, 9728)
+    x = make_baseline_activations(rows, 2560, SEED, outliers=True)
+    wgu, sgu = make_baseline_weights(gu_shape, SEED)
+    wd, sd = make_baseline_weights(down_shape, SEED + 1)
+    xg = x.to(gpu)
+    out = fp8.mlp_forward_mi355x_fp8(xg, wgu.to(gpu), sgu.to(gpu), wd.to(gpu), sd.to(gpu))
+    # Reference chain on the oracle, stage by stage, each against the GPU's intermediate.
+    gate_up = fp8.mi355x_fp8_linear(xg, wgu.to(gpu), sgu.to(gpu), [128, 128])
+    assert_close_rows(gate_up, oracle_linear(x, wgu, sgu))
+    h, q, s = fp8.silu_mul_quant_mi355x_fp8(gate_up[:, :9728], gate_up[:, 9728:], return_intermediate=True)
+    q_ref, s_ref = oracle.act_quant(bits16(h))
+    assert np.array_equal(codes(q), q_ref)
+    down_ref = oracle.block_gemm(q_ref, s_ref, codes(wd), sd.numpy())
+    assert_close_rows(out, _bf16(down_ref))
+
+
+@pytest.mark.parametrize("rows", [1, 8, 100, 300, 2048])
+def test_merged_projections_equal_separate_bitwise(gpu, rows):
+    _note("merged", rows)
+
+    class Lin(torch.nn.Module):
+        def __init__(self, n, k, seed):
+            super().__init__()
+            w, s = make_weights(ModelShape("p", n, k), seed)
+            self.weight = torch.nn.Parameter(w.to(gpu), requires_grad=False)
+            self.register_buffer("weight_scale_inv", s.to(gpu))
+            self.block_size = (128, 128)
+            self.bias = None
+            self.activation_scale = None
+
+        def forward(self, x):
+            return fp8.mi355x_fp8_linear(x, self.weight, self.weight_scale_inv, list(self.block_size))
+
+    attn = torch.nn.Module()
+    attn.q_proj, attn.k_proj, attn.v_proj = Lin(4096, 2560, 1), Lin(1024, 2560, 2), Lin(1024, 2560, 3)
+    mlp = torch.nn.Module()
+    mlp.gate_proj, mlp.up_proj = Lin(9728, 2560, 4), Lin(9728, 2560, 5)
+    model = torch.nn.Module()
+    model.attn, model.mlp = attn, mlp
+    x = make_activations(rows, 2560, SEED).to(gpu)
+    separate = [attn.q_proj(x), attn.k_proj(x), attn.v_proj(x), mlp.gate_proj(x), mlp.up_proj(x)]
+    assert mp.install_merged_projections(model) == 2
+    merged = list(mp.project_qkv(attn, x)) + list(mp.project_gate_up(mlp, x))
+    for got, ref in zip(merged, separate):
+        assert bitwise_equal(got.contiguous(), ref), rows

@@ -190,3 +190,17 @@ def test_linear_row_independence_and_fp16_output():
     bf = torch.from_numpy(full.view(np.int16)).view(torch.bfloat16).float()
     finite = torch.isfinite(hf)
     assert torch.allclose(hf[finite], bf[finite], rtol=2 ** -7, atol=1e-3)
+
+
+def test_silu_mul_matches_torch_bf16_semantics():
+    """The reference's silu_mul is PyTorch's bf16 F.silu(g) * u (fused.py:135-137):
+    torch on CPU computes silu in fp32 and rounds to bf16, then multiplies in bf16."""
+
+    gen = torch.Generator().manual_seed(3)
+    g = (torch.randn(4096, generator=gen) * 4).to(torch.bfloat16)
+    u = (torch.randn(4096, generator=gen) * 2).to(torch.bfloat16)
+    g[:6] = torch.tensor([0.0, -0.0, 88.0, -88.0, 1e-30, -100.0]).to(torch.bfloat16)
+    ours = oracle.silu_mul(bits16(g), bits16(u))
+    ref = bits16(torch.nn.functional.silu(g) * u)
+    ulps = np.abs(ours.astype(np.int32) - ref.astype(np.int32))
+    assert ulps.max() <= 1 and (ulps == 0).mean() > 0.99
