@@ -6,16 +6,22 @@ merged Qwen3-4B projections (qkv, o_proj, gate_up, down), on one GPU.
 * A step is one pass of the block GEMM over the four projections for one batch: the
   prefill step at M=2048 (``value`` = TFLOPS = sum 2MNK / sum GEMM time) and the decode
   step at M=8 (``decode.gbps`` = op-level bytes / GEMM time).  Activations are quantized
-  before the timed region (the quantizer is timed separately, ``quant``) and all inputs
-  are resident in HBM.
-* Weights rotate through enough independent sets (> 512 MB) that no step reads weights
-  that are still in the 256 MB MALL from the step before.
-* Timing: each projection's launches (one per weight set) are captured in a HIP graph
-  and replayed K times between two HIP events recorded on the stream the kernels run on;
-  the per-launch time is the elapsed time over K x sets launches, so
-  ``roofline.achieved`` is the average per-launch rate of the dominant kernel.
-* ``cpu_baseline`` times the C oracle (a CPU restatement of the reference arithmetic) on
-  a bounded sample: the same four projections at ``--cpu-rows`` rows.
+  before the timed region (the quantizer is timed separately, ``quant``) and all inputs are
+  resident in HBM.  The GEMM reads K-group-major activation scales, the layout
+  ``fp8_linear`` hands it.
+* Weights rotate through enough independent sets (> 512 MB) that no launch reads weights
+  still in the 256 MB MALL from the launch before.
+* Timing: each projection's launches (one per weight set) are captured in a HIP graph and
+  replayed K times between two HIP events recorded on the stream the kernels run on; the
+  per-launch time is the elapsed time over K x sets launches, so ``roofline.achieved`` is
+  the average per-launch rate of the dominant kernel.
+* Also reported: baseline config 4 (the MLP block at M=512: gate_up -> SiLU*up + requant ->
+  down, ``extras.mlp``) and config 5 (one continuous-batching step of the 36-layer linear
+  stack, 144 full linears with independent weights at M = 512 + 24 = 536, ``extras.stack``).
+* ``cpu_baseline`` times the C oracle (a CPU restatement of the reference arithmetic) on a
+  bounded sample: the same four projections at ``--cpu-rows`` rows.
+* ``roofline.traffic`` / ``roofline_decode.traffic`` are the measured HBM bytes per launch
+  from the committed rocprofv3 PMC summary (profiles/hbm_traffic_qwen3.txt), when present.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
 """
@@ -36,6 +42,7 @@ for _p in (os.path.join(ROOT, "mini-inference-engine_amd"), os.path.join(ROOT, "
 PEAK_FP8_TFLOPS = 5000.0   # MI355X dense OCP-FP8 MFMA
 PEAK_HBM_GBPS = 8000.0     # MI355X HBM3E
 SEED = 20261008
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic_qwen3.txt")
 
 
 def parse_args(argv=None):
@@ -46,8 +53,52 @@ def parse_args(argv=None):
     p.add_argument("--prefill-m", type=int, default=2048)
     p.add_argument("--decode-m", type=int, default=8)
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    p.add_argument("--cpu-rows", type=int, default=1024)
+    p.add_argument("--cpu-rows", type=int, default=4096)
+    p.add_argument("--no-extras", action="store_true", help="skip the MLP-block and 36-layer-stack configs")
+    p.add_argument("--eager", action="store_true",
+                   help="launch kernels directly instead of through HIP graphs (for counter collection)")
+    p.add_argument("--only", choices=["prefill", "decode"], help="time one phase only")
+    p.add_argument("--copy-calibration", type=int, metavar="MIB", default=0,
+                   help="only run a device-to-device copy of MIB MiB a few times (PMC calibration) and exit")
     return p.parse_args(argv)
+
+
+def timed_graph(torch, stream, fn, launches_per_call, steps, warmup, eager):
+    """Average ms per launch of ``fn`` (which issues ``launches_per_call`` launches)."""
+
+    with torch.cuda.stream(stream):
+        fn()  # warm-up outside capture: sizes workspaces, so the capture allocates nothing new
+        stream.synchronize()
+        if eager:
+            run = fn
+        else:
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph, stream=stream):
+                fn()
+            run = graph.replay
+        for _ in range(warmup):
+            run()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        stream.synchronize()
+        start.record(stream)
+        for _ in range(steps):
+            run()
+        end.record(stream)
+        end.synchronize()
+    return start.elapsed_time(end) / (steps * launches_per_call)
+
+
+def read_traffic():
+    """Bytes per launch measured by rocprofv3 (FETCH_SIZE + WRITE_SIZE, calibrated), from
+    the committed summary: lines ``TRAFFIC <phase> <projection> <bytes>``."""
+
+    out = {}
+    if os.path.exists(TRAFFIC_FILE):
+        for line in open(TRAFFIC_FILE):
+            parts = line.split()
+            if len(parts) == 4 and parts[0] == "TRAFFIC":
+                out[(parts[1], parts[2])] = float(parts[3])
+    return out
 
 
 def main(argv=None) -> int:
@@ -71,72 +122,47 @@ def main(argv=None) -> int:
         print("bench.py needs an MI355X (gfx950) GPU", file=sys.stderr)
         return 2
     torch.cuda.set_device(dev)
+    stream = torch.cuda.Stream()
+
+    if args.copy_calibration:
+        n = args.copy_calibration << 20
+        src = torch.ones(n, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration_bytes": n, "launches": 5}), flush=True)
+        return 0
+
     projs = QWEN3_4B_PROJECTIONS
     layer_bytes = sum(p.n * p.k for p in projs)
     sets = max(2, -(-512 * 2**20 // layer_bytes) + 1)
     print(f"generating {sets} weight sets of {layer_bytes / 2**20:.1f} MiB", file=sys.stderr, flush=True)
     weights = [[make_baseline_weights(p, SEED + 1000 * s, device="cuda") for p in projs] for s in range(sets)]
 
-    def prepare(m, outliers):
-        xs, qs, out = [], [], []
-        for p in projs:
-            x = make_baseline_activations(m, p.k, SEED, outliers=outliers, device="cuda")
-            xs.append(x)
-            qs.append(fp8.quantize_mi355x_fp8_activation(x, scale_layout="kgroup"))
-            out.append(torch.empty((m, p.n), dtype=torch.bfloat16, device=dev))
-        return xs, qs, out
-
     def run_phase(m, outliers):
-        """Per projection: one HIP graph of `sets` back-to-back GEMM launches (one per
-        weight set), replayed `steps` times between two HIP events on the launch stream.
-        Graph replay removes the host's launch gaps, so the events time the kernels."""
+        per_launch, quant = [], []
+        for i, p in enumerate(projs):
+            x = make_baseline_activations(m, p.k, SEED, outliers=outliers, device="cuda")
+            q, s = fp8.quantize_mi355x_fp8_activation(x, scale_layout="kgroup")
+            out = torch.empty((m, p.n), dtype=torch.bfloat16, device=dev)
 
-        xs, qs, outs = prepare(m, outliers)
-        stream = torch.cuda.Stream()
-        per_launch_ms, graphs = [], []
-        with torch.cuda.stream(stream):
-            for i, p in enumerate(projs):
-                for r in range(sets):  # eager warm-up outside capture
-                    fp8.launch_block_gemm(qs[i][0], weights[r][i][0], outs[i], qs[i][1], weights[r][i][1])
-                stream.synchronize()
-                graph = torch.cuda.CUDAGraph()
-                with torch.cuda.graph(graph, stream=stream):
-                    for r in range(sets):
-                        fp8.launch_block_gemm(qs[i][0], weights[r][i][0], outs[i], qs[i][1], weights[r][i][1])
-                graphs.append(graph)
-            for i, p in enumerate(projs):
-                for _ in range(args.warmup):
-                    graphs[i].replay()
-                start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-                stream.synchronize()
-                start.record(stream)
-                for _ in range(args.steps):
-                    graphs[i].replay()
-                end.record(stream)
-                end.synchronize()
-                per_launch_ms.append(start.elapsed_time(end) / (args.steps * sets))
-            # Quantizer timing (separate: not part of the GEMM metric).
-            quant_ms = []
-            for i, p in enumerate(projs):
-                fp8.quantize_mi355x_fp8_activation(xs[i], scale_layout="kgroup")
-                graph = torch.cuda.CUDAGraph()
-                with torch.cuda.graph(graph, stream=stream):
-                    for _ in range(sets):
-                        fp8.quantize_mi355x_fp8_activation(xs[i], scale_layout="kgroup")
-                graph.replay()
-                start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-                stream.synchronize()
-                start.record(stream)
-                for _ in range(args.steps):
-                    graph.replay()
-                end.record(stream)
-                end.synchronize()
-                quant_ms.append(start.elapsed_time(end) / (args.steps * sets))
-        torch.cuda.synchronize()
-        return per_launch_ms, quant_ms
+            def gemms(i=i, q=q, s=s, out=out):
+                for r in range(sets):
+                    fp8.launch_block_gemm(q, weights[r][i][0], out, s, weights[r][i][1])
+
+            def quants(x=x):
+                for _ in range(sets):
+                    fp8.quantize_mi355x_fp8_activation(x, scale_layout="kgroup")
+
+            per_launch.append(timed_graph(torch, stream, gemms, sets, args.steps, args.warmup, args.eager))
+            quant.append(timed_graph(torch, stream, quants, sets, args.steps, args.warmup, args.eager))
+        return per_launch, quant
 
     results = {}
     for phase, m, outliers in (("prefill", args.prefill_m, True), ("decode", args.decode_m, False)):
+        if args.only and phase != args.only:
+            continue
         print(f"timing {phase} M={m}", file=sys.stderr, flush=True)
         mean, quant_ms = run_phase(m, outliers)
         flops = [linear_flops(m, p.n, p.k) for p in projs]
@@ -146,16 +172,32 @@ def main(argv=None) -> int:
             "step_ms": sum(mean),
             "tflops": sum(flops) / (sum(mean) * 1e9),
             "gbps": sum(nbytes) / (sum(mean) * 1e6),
-            "per_proj": {p.name: {"mean_us": 1e3 * mean[i],
-                                  "tflops": flops[i] / (mean[i] * 1e9), "gbps": nbytes[i] / (mean[i] * 1e6)}
+            "per_proj": {p.name: {"mean_us": 1e3 * mean[i], "tflops": flops[i] / (mean[i] * 1e9),
+                                  "gbps": nbytes[i] / (mean[i] * 1e6), "algorithmic_bytes": nbytes[i],
+                                  "flops": flops[i]}
                          for i, p in enumerate(projs)},
             "quant": {p.name: {"us": 1e3 * quant_ms[i], "gbps": quant_bytes(m, p.k) / (quant_ms[i] * 1e6)}
                       for i, p in enumerate(projs)},
         }
+    if args.only:
+        print(json.dumps({"phase": args.only, "detail": results}), flush=True)
+        return 0
+    del weights
+    torch.cuda.empty_cache()
 
-    cpu = None
-    if not args.no_cpu:
-        cpu = cpu_baseline(args.cpu_rows)
+    extras = {}
+    if not args.no_extras:
+        print("timing MLP block and 36-layer stack", file=sys.stderr, flush=True)
+        extras["mlp"] = bench_mlp(torch, fp8, stream, args, make_baseline_weights, make_baseline_activations)
+        extras["stack"] = bench_stack(torch, fp8, stream, args, make_baseline_weights, make_baseline_activations,
+                                      projs)
+
+    cpu = None if args.no_cpu else cpu_baseline(args.cpu_rows)
+    traffic = read_traffic()
+
+    def traffic_per_launch(phase):
+        vals = [traffic.get((phase, p.name)) for p in projs]
+        return None if any(v is None for v in vals) else round(sum(vals) / len(vals))
 
     pre, dec = results["prefill"], results["decode"]
     line = {
@@ -177,17 +219,61 @@ def main(argv=None) -> int:
                    "prefill_m": pre["m"], "decode_m": dec["m"], "weight_sets": sets},
         "decode": {"gbps": round(dec["gbps"], 1), "ms_per_step": round(dec["step_ms"], 4),
                    "frac_of_hbm": round(dec["gbps"] / PEAK_HBM_GBPS, 4)},
-        "roofline": {"bound": "mfma", "kernel": "tile_gemm_kernel (prefill M=2048, 4 projections)",
+        "roofline": {"bound": "mfma", "kernel": "prefill block GEMM (M=2048, mean over the 4 projections)",
                      "achieved": round(pre["tflops"], 2), "peak": PEAK_FP8_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(pre["tflops"] / PEAK_FP8_TFLOPS, 4), "traffic": None},
-        "roofline_decode": {"bound": "hbm", "kernel": "stream_gemm_kernel (decode M=8, 4 projections)",
+                     "frac": round(pre["tflops"] / PEAK_FP8_TFLOPS, 4), "traffic": traffic_per_launch("prefill")},
+        "roofline_decode": {"bound": "hbm", "kernel": "stream_gemm_kernel (decode M=8, mean over the 4 projections)",
                             "achieved": round(dec["gbps"], 1), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
-                            "frac": round(dec["gbps"] / PEAK_HBM_GBPS, 4), "traffic": None},
+                            "frac": round(dec["gbps"] / PEAK_HBM_GBPS, 4), "traffic": traffic_per_launch("decode")},
+        "extras": extras,
         "detail": results,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
     return 0
+
+
+def bench_mlp(torch, fp8, stream, args, make_w, make_x):
+    """Baseline config 4: x[512, 2560] -> gate_up -> SiLU(gate)*up + requant -> down."""
+
+    from minillm_amd.validation import QWEN3_4B_PROJECTIONS
+
+    gu, down = QWEN3_4B_PROJECTIONS[2], QWEN3_4B_PROJECTIONS[3]
+    m = 512
+    wgu, sgu = make_w(gu, SEED, device="cuda")
+    wd, sd = make_w(down, SEED + 1, device="cuda")
+    x = make_x(m, gu.k, SEED, outliers=True, device="cuda")
+    ms = timed_graph(torch, stream, lambda: fp8.mlp_forward_mi355x_fp8(x, wgu, sgu, wd, sd), 1, args.steps,
+                     args.warmup, args.eager)
+    flops = 2 * m * (gu.n * gu.k + down.n * down.k)
+    return {"config": "MLP block M=512 (gate_up, fused SiLU*up + requant, down; incl. the input quantizer)",
+            "us": round(ms * 1e3, 2), "tflops": round(flops / (ms * 1e9), 1)}
+
+
+def bench_stack(torch, fp8, stream, args, make_w, make_x, projs):
+    """Baseline config 5: 36 layers x 4 full linears (quantizer + GEMM), independent weights,
+    M = 512-token prefill chunk + 24 decode tokens = 536."""
+
+    m, layers = 536, 36
+    weights = [[make_w(p, SEED + 7919 * layer + i, device="cuda") for i, p in enumerate(projs)]
+               for layer in range(layers)]
+    xs = [make_x(m, p.k, SEED + i, outliers=True, device="cuda") for i, p in enumerate(projs)]
+
+    def step():
+        for layer in range(layers):
+            for i in range(len(projs)):
+                w, s = weights[layer][i]
+                fp8.mi355x_fp8_linear(xs[i], w, s, [128, 128])
+
+    ms = timed_graph(torch, stream, step, 1, max(2, args.steps // 4), 2, args.eager)
+    flops = layers * sum(2 * m * p.n * p.k for p in projs)
+    nbytes = layers * sum(p.n * p.k for p in projs)
+    del weights
+    torch.cuda.empty_cache()
+    return {"config": "36-layer linear stack, 144 linears (quantizer + GEMM), M=536, independent weights",
+            "ms": round(ms, 3), "tflops": round(flops / (ms * 1e9), 1),
+            "weight_gbps": round(nbytes / (ms * 1e6), 1),
+            "frac_of_fp8_peak": round(flops / (ms * 1e9) / PEAK_FP8_TFLOPS, 4)}
 
 
 def cpu_baseline(rows: int) -> dict:
