@@ -19,7 +19,7 @@
 //                       streaming: each workgroup owns 16 or 32 W rows over the whole of
 //                       K, W goes global -> registers (every byte read once, D K groups in
 //                       flight per wave), the small activation matrix is served from L2,
-//                       and the eight waves' K-partials combine in LDS.  No workspace, no
+//                       and the sixteen waves' K-partials combine in LDS.  No workspace, no
 //                       cross-workgroup synchronisation.
 //   tile_gemm_kernel    prefill-sized M.  MFMA-bound: 128x128 output tile per 256-thread
 //                       workgroup, 2x2 waves of 64x64, K groups staged global -> registers

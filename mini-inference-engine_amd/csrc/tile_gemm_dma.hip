@@ -6,15 +6,16 @@
 // 256-thread workgroup, 2x2 waves of 64x64.
 //
 // What differs is the feed: global memory goes straight into LDS with
-// global_load_lds_dwordx4 (no register staging, no ds_write), through a ring of three
-// stages, so the loads of K group kb+2 are in flight while kb is multiplied.  Each stage
+// global_load_lds_dwordx4 (no register staging, no ds_write), through a ring of STAGES
+// stages (2 as launched, two workgroups per CU; 3 is kept as a template option), so the
+// loads of K group kb+STAGES-1 are in flight while kb is multiplied.  Each stage
 // holds the W tile (128 rows x 128 B), the activation tile (128 x 128 B) and the 128
 // activation scales of its K group.  A 64-lane DMA instruction fills 1 KiB of LDS
 // linearly (lane i -> byte 16 i), i.e. 8 rows of 8 16-byte chunks; the XOR swizzle
 // (physical chunk p of row r holds logical chunk p ^ (r & 7)) is applied by choosing each
 // lane's source address, so the MFMA fragment reads (ds_read_b128) are bank-conflict free.
 //
-// The three stages are distinct LDS objects and the K loop is unrolled by three, so the
+// The stages are distinct LDS objects and the K loop is unrolled by STAGES, so the
 // compiler can tell the stages apart and does not wait for in-flight DMA before reading
 // the current stage; the waits are explicit (vmcnt) before each workgroup barrier.
 //
