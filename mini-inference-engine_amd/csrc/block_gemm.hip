@@ -301,6 +301,48 @@ int plan_gemm(int64_t M, int64_t N, int64_t K, int config, GemmPlan* plan) {
 
 size_t gemm_workspace_bytes(const GemmPlan&) { return 0; }
 
+int64_t device_cus() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
+
+// Prefill kernel choice when the LDS-DMA kernels can run: the 256-row kernel at its best
+// tile width (256, 224 or 192), or the 128-row kernel (two workgroups per CU) at width 128,
+// 160 or 64, whichever has the smallest cost = the largest per-CU share of padded tile area,
+// ceil(tiles / CUs) x rows x width, with the 128-row kernel's weighted by 1.2 for its
+// lower MFMA rate per CU.  On the Qwen3-4B shapes at M = 2048 this picks 256x192 for qkv
+// (256 tiles), 256x224 for gate_up (696), 128x160 for o_proj and down (256).
+#ifndef MI355X_PREFILL_POLICY
+#define MI355X_PREFILL_POLICY 0  // 0: cost model, 1: always 256-row, 2: always 128-row
+#endif
+struct PrefillChoice {
+  bool rows256;
+  int bn;
+};
+static PrefillChoice choose_prefill(int64_t M, int64_t N, int64_t cus) {
+  const int bn256 = tile256_width(M, N, cus);
+  const int64_t cost256 = cdiv(cdiv(M, 256) * cdiv(N, bn256), cus) * 256 * bn256;
+  int bn128 = 128;
+  int64_t cost128 = 0;
+  for (int bn : {128, 160, 64}) {
+    const int64_t cost = cdiv(cdiv(M, 128) * cdiv(N, bn), cus) * 128 * bn * 6 / 5;
+    if (cost128 == 0 || cost < cost128) {
+      cost128 = cost;
+      bn128 = bn;
+    }
+  }
+  if (MI355X_PREFILL_POLICY == 1) return {true, bn256};
+  if (MI355X_PREFILL_POLICY == 2) return {false, bn128};
+  return cost256 <= cost128 ? PrefillChoice{true, bn256} : PrefillChoice{false, bn128};
+}
+
 template <int NT, int AF, bool ALIGNED, typename OutT>
 static void launch_stream_t(const uint8_t* q, int64_t ldq, const float* as, int64_t as_sm, int64_t as_sk,
                             const uint8_t* w, int64_t ldw, const float* ws, int64_t ws_sn, int64_t ws_sk,
@@ -365,16 +407,14 @@ int launch_block_gemm(const GemmPlan& plan, const uint8_t* q, int64_t ldq, const
   const bool dma_ok = tile_dma_supported(q, ldq, as_sm, as_sk, w, ldw, M, K);
   if (plan.kernel == MI355X_FP8_CONFIG_TILE256) {
     if (!dma_ok) return MI355X_FP8_ERR_UNSUPPORTED;
-    return launch_tile256(q, ldq, as, as_sk, w, ldw, ws, ws_sn, ws_sk, out, out_dtype, ldo, M, N, K, stream);
+    return launch_tile256(q, ldq, as, as_sk, w, ldw, ws, ws_sn, ws_sk, out, out_dtype, ldo, M, N, K,
+                          tile256_width(M, N, device_cus()), stream);
   }
   if (plan.kernel == MI355X_FP8_CONFIG_TILE128 && dma_ok) {
-    // 256x256 tiles halve the L2 traffic per flop but leave CUs idle when there are few
-    // of them; below about 160 tiles (o_proj and down at M=2048: 80) the 128x128 kernel,
-    // two workgroups per CU, finishes first.
-    const int64_t tiles256 = cdiv(M, 256) * cdiv(N, 256);
-    if (tiles256 >= 160)
-      return launch_tile256(q, ldq, as, as_sk, w, ldw, ws, ws_sn, ws_sk, out, out_dtype, ldo, M, N, K, stream);
-    return launch_tile_dma(q, ldq, as, as_sk, w, ldw, ws, ws_sn, ws_sk, out, out_dtype, ldo, M, N, K, stream);
+    const PrefillChoice c = choose_prefill(M, N, device_cus());
+    if (c.rows256)
+      return launch_tile256(q, ldq, as, as_sk, w, ldw, ws, ws_sn, ws_sk, out, out_dtype, ldo, M, N, K, c.bn, stream);
+    return launch_tile_dma(q, ldq, as, as_sk, w, ldw, ws, ws_sn, ws_sk, out, out_dtype, ldo, M, N, K, c.bn, stream);
   }
   const bool aligned = (K % 16) == 0 && (ldq % 16) == 0 && (ldw % 16) == 0 &&
                        (reinterpret_cast<uintptr_t>(q) % 16) == 0 &&

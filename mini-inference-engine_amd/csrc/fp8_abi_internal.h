@@ -37,14 +37,20 @@ int launch_block_gemm(const GemmPlan& plan, const uint8_t* q, int64_t ldq, const
 // LDS-DMA pipelined prefill kernel (tile_gemm_dma.hip) and its preconditions.
 bool tile_dma_supported(const uint8_t* q, int64_t ldq, int64_t as_sm, int64_t as_sk, const uint8_t* w,
                         int64_t ldw, int64_t M, int64_t K);
+// bn: tile width, 64, 128 or 160.
 int launch_tile_dma(const uint8_t* q, int64_t ldq, const float* as, int64_t as_sk, const uint8_t* w,
                     int64_t ldw, const float* ws, int64_t ws_sn, int64_t ws_sk, void* out, int out_dtype,
-                    int64_t ldo, int64_t M, int64_t N, int64_t K, hipStream_t stream);
+                    int64_t ldo, int64_t M, int64_t N, int64_t K, int bn, hipStream_t stream);
 
-// 256x256-tile prefill kernel (tile_gemm_256.hip); same preconditions as the DMA kernel.
+// 256-row-tile prefill kernel (tile_gemm_256.hip); same preconditions as the DMA kernel.
+// bn: tile width, 256, 224 or 192 (tile256_width picks the one that best fills `cus` CUs).
 int launch_tile256(const uint8_t* q, int64_t ldq, const float* as, int64_t as_sk, const uint8_t* w,
                    int64_t ldw, const float* ws, int64_t ws_sn, int64_t ws_sk, void* out, int out_dtype,
-                   int64_t ldo, int64_t M, int64_t N, int64_t K, hipStream_t stream);
+                   int64_t ldo, int64_t M, int64_t N, int64_t K, int bn, hipStream_t stream);
+int tile256_width(int64_t M, int64_t N, int64_t cus);
+
+// Compute units of the current device (cached per device; 256 if it cannot be queried).
+int64_t device_cus();
 
 inline size_t align256(size_t v) { return (v + 255) & ~static_cast<size_t>(255); }
 

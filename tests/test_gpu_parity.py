@@ -246,3 +246,30 @@ def test_prefill_2048_full_size(gpu, shape):
     dense = _dense(xg[sample], wg, wsg, shape.n, shape.k)
     ours, oracle_err = _rel_l2(out[sample], dense), _rel_l2(expected.to(gpu), dense)
     assert (ours <= 1.25 * oracle_err + 1e-4).all(), (ours.tolist(), oracle_err.tolist())
+
+
+@pytest.mark.parametrize("rows,n,k", [
+    (536, 2560, 4096),    # stack-step o_proj: 128x64 tiles
+    (300, 200, 256),      # row and column tails, 128x64 tiles
+    (2048, 2560, 256),    # o_proj / down width: 128x160 tiles (weight-scale blocks straddled)
+    (2048, 6144, 256),    # qkv width: 256x192 tiles
+    (2048, 19456, 128),   # gate_up width: 256x224 tiles, last tile partial
+    (2048, 8192, 128),    # 256x256 tiles
+], ids=lambda v: str(v))
+def test_prefill_tile_widths(gpu, rows, n, k):
+    """Every tile width the prefill dispatch picks, against the oracle (the widths follow
+    from the shapes: see choose_prefill in block_gemm.hip)."""
+
+    _note("widths", rows, n, k)
+    shape = ModelShape("w", n, k)
+    x = make_baseline_activations(rows, k, SEED + rows, outliers=True)
+    w, ws = make_baseline_weights(shape, SEED + n)
+    wg, wsg = w.to(gpu), ws.to(gpu)
+    out = fp8.mi355x_fp8_linear(x.to(gpu), wg, wsg, BLOCK)
+    assert_close_rows(out, oracle_linear(x, w, ws))
+    # Bitwise equal to the register-staged 128x128 kernel, which row-major activation
+    # scales select (same per-element fold, different tiling and feed).
+    q, s_row = fp8.quantize_mi355x_fp8_activation(x.to(gpu))
+    reg = torch.empty_like(out)
+    fp8.launch_block_gemm(q, wg, reg, s_row, wsg)
+    assert bitwise_equal(reg, out), bit_mismatch_details(reg, out)
