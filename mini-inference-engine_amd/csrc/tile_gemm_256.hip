@@ -112,6 +112,22 @@ __device__ __forceinline__ void issue256(const Src256& src, const uint8_t* w, co
   for (int i = 0; i < 4; ++i) dma16(qk, src.x[i], st + G::kXOff + (i * 8 + wave) * 64);
 }
 
+// One of the step's DMA instructions: t < kWPerWave loads W block 8 t + wave, the rest the
+// activation blocks.
+template <int BN, int S>
+__device__ __forceinline__ void issue_one(const Src256& src, const uint8_t* w, const uint8_t* q, int64_t kb, int wave,
+                                          int t) {
+  using G = Geo<BN>;
+  uint4* st = stage256<S>();
+  if (t < G::kWPerWave) {
+    const int blk = (t * 8 + wave) < G::kWBlocks ? (t * 8 + wave) : (G::kWBlocks - 1);
+    dma16(w + kb * kGroup, src.w[t], st + blk * 64);
+  } else {
+    const int i = t - G::kWPerWave;
+    dma16(q + kb * kGroup, src.x[i], st + G::kXOff + (i * 8 + wave) * 64);
+  }
+}
+
 template <int S>
 __device__ __forceinline__ v8i frag(const uint4* tile, int row, int g) {
   const uint4* p = tile + row * 8;
@@ -128,12 +144,17 @@ struct Scales {
 // The wave's four activation fragments stay in registers for the whole K group; the W
 // fragments stream through two ahead, each feeding four independent MFMAs.  Read order:
 // the first W fragment, then the four activation fragments, then the second W fragment,
-// so the first MFMA waits for two fragments, not for all of them.
+// so the first MFMA waits for two fragments, not for all of them.  The DMA loads of the
+// next K group (into the other stage, kn) go out in two halves, before the first and
+// before the middle MFMA group: a wave then never sits behind its whole DMA batch while
+// its partner wave on the SIMD does the same (measured 2-5 % faster than one batch).
 template <int BN, int S>
 __device__ __forceinline__ void compute256(v4f (&acc)[Geo<BN>::kNI][4], const Scales& sc_in, uint32_t use_b, int wm,
-                                           int wn, int r, int g) {
+                                           int wn, int r, int g, const Src256& src, const uint8_t* w,
+                                           const uint8_t* q, int64_t kn, int wave) {
   using G = Geo<BN>;
   constexpr int NI = G::kNI;
+  constexpr int NDMA = G::kWPerWave + 4;
   const uint4* st = stage256<S>();
   const int wrow0 = wn * (BN / 2) + r;
   v8i a0 = frag<S>(st, wrow0, g);
@@ -143,6 +164,9 @@ __device__ __forceinline__ void compute256(v4f (&acc)[Geo<BN>::kNI][4], const Sc
   v8i a1 = frag<S>(st, wrow0 + 16, g);
 #pragma unroll
   for (int i = 0; i < NI; ++i) {
+#pragma unroll
+    for (int t = 0; t < NDMA; ++t)
+      if ((t < NDMA / 2 ? 0 : NI / 2) == i) issue_one<BN, S ^ 1>(src, w, q, kn, wave, t);
     v8i a2;
     if (i + 2 < NI) a2 = frag<S>(st, wrow0 + 16 * (i + 2), g);
     const float wsv = (use_b >> i) & 1 ? sc_in.wb : sc_in.wa;
@@ -179,7 +203,7 @@ __device__ __forceinline__ void load_scales(Scales& s, const Src256& src, int64_
 }
 
 // One K group kb of the range [.., khi).  The scales of K group kb + 1 go to registers
-// (per-lane loads, L2 hits), issued before the DMA batch so that the end-of-step wait also
+// (per-lane loads, L2 hits), issued before the DMA loads so that the end-of-step wait also
 // covers them; the two unrolled steps alternate between two register sets.  Past the end
 // of the range the loads repeat its last group (the stage they fill is not read again).
 template <int BN, int CUR>
@@ -189,12 +213,14 @@ __device__ __forceinline__ void step256(v4f (&acc)[Geo<BN>::kNI][4], const Scale
                                         int g) {
   const int64_t kn = kb + 1 < khi ? kb + 1 : khi - 1;
   load_scales(next, src, kn, as_sk, ws_sk);
-  // Keep the issue order scales, DMA batch (compiler and scheduler barriers).
+  // Keep the scale loads ahead of the DMA loads (compiler and scheduler barriers).
   asm volatile("" ::: "memory");
   __builtin_amdgcn_sched_barrier(0);
-  issue256<BN, CUR ^ 1>(src, w, q, kn, wave);
+  compute256<BN, CUR>(acc, cur, src.use_b, wm, wn, r, g, src, w, q, kn, wave);
+  // Every MFMA of the step is issued before the wait: the matrix core then works through
+  // them while the wave waits for its DMA and the other waves (without this barrier the
+  // scheduler moves the last MFMA groups behind s_barrier; measured 7 % slower on qkv).
   __builtin_amdgcn_sched_barrier(0);
-  compute256<BN, CUR>(acc, cur, src.use_b, wm, wn, r, g);
   sync_stage();
 }
 

@@ -168,6 +168,9 @@ __device__ __forceinline__ void k_step(v4f (&acc)[DmaGeo<BN>::kNI][4], const Dma
   const int64_t ahead = kb + STAGES - 1;
   issue_stage<BN, NXT>(src, ahead < KB ? ahead : KB - 1, as_sk, wave, lane);
   if (kb < KB) compute_stage<BN, CUR>(acc, src.ws_a[kb * ws_sk], src.ws_b[kb * ws_sk], src.use_b, wm, wn, r, g);
+  // Keep this step's MFMAs ahead of the next step's wait and barrier, so the matrix core
+  // works through them while the wave waits (measured 6 % faster on o_proj and down).
+  __builtin_amdgcn_sched_barrier(0);
 }
 
 template <int STAGES, int BN, typename OutT>
