@@ -110,3 +110,33 @@ def test_merged_projections_equal_separate_bitwise(gpu, rows):
     merged = list(mp.project_qkv(attn, x)) + list(mp.project_gate_up(mlp, x))
     for got, ref in zip(merged, separate):
         assert bitwise_equal(got.contiguous(), ref), rows
+
+
+def test_checkpoint_loader_feeds_the_linear(gpu, tmp_path):
+    """Weights loaded from a safetensors checkpoint straight into HBM run through the
+    linear: merged q/k/v against the oracle, and its column ranges bitwise equal to the
+    separately loaded projections."""
+
+    from safetensors.torch import save_file
+
+    from minillm_amd import checkpoint as ckpt
+
+    gen = torch.Generator().manual_seed(11)
+    tensors = {}
+    for module, n in (("self_attn.q_proj", 512), ("self_attn.k_proj", 128), ("self_attn.v_proj", 128)):
+        w, s = make_weights(ModelShape(module, n, 384), 11 + n)
+        tensors[f"model.layers.0.{module}.weight"] = w
+        tensors[f"model.layers.0.{module}.weight_scale_inv"] = s.to(torch.float16)
+    save_file(tensors, str(tmp_path / "model.safetensors"))
+    ck = ckpt.FP8Checkpoint(str(tmp_path))
+    w, s = ck.projection(0, ckpt.PROJECTIONS["qkv"], device=gpu)
+    assert w.is_cuda and s.dtype == torch.float32
+    x = make_activations(40, 384, 7)
+    out = fp8.mi355x_fp8_linear(x.to(gpu), w, s, [128, 128])
+    assert_close_rows(out, oracle_linear(x, w.cpu(), s.cpu()))
+    row = 0
+    for module in ckpt.PROJECTIONS["qkv"]:
+        wp, sp = ck.projection(0, (module,), device=gpu)
+        part = fp8.mi355x_fp8_linear(x.to(gpu), wp, sp, [128, 128])
+        assert bitwise_equal(part, out[:, row:row + wp.shape[0]].contiguous())
+        row += wp.shape[0]
