@@ -113,6 +113,28 @@ int mi355x_fp8_silu_mul_quant(const void* gate, const void* up, int x_dtype, int
                               int64_t ld, void* h, int64_t ldh, uint8_t* q, int64_t ldq, int64_t kpad,
                               float* s, int64_t s_sm, int64_t s_sk, void* stream);
 
+/*
+ * Fused RMSNorm (optionally after the residual add) followed by the activation quantizer,
+ * the input of the q/k/v and gate/up projections.  Replaces rms_norm
+ * (engine/kernels/fused.py:89-124, 165-199) plus the quantizer launch of the projection
+ * that consumes its output (engine/kernels/sm89_fp8.py:401-424).
+ *   x        : M x K bf16, (m, k) at x[m*sxm + k]; K % 4 == 0 and K >= 128
+ *   residual : optional (NULL: none) M x K bf16 at residual[m*ldr + k]; then residual_out
+ *              (m, k) at residual_out[m*ldro + k] receives bf16(x + residual), the input
+ *              of the normalization
+ *   weight   : K bf16 (the norm's gain)
+ *   y        : optional (NULL: not written) bf16 normalized output at y[m*ldy + k]
+ *   q, s     : quantized normalized output and its raw fp32 scales, as in mi355x_fp8_act_quant
+ * The row sum follows PyTorch's reduction order for M rows of width K; 1/sqrt is correctly
+ * rounded (the reference's libdevice rsqrt is approximate: y can differ in the last bf16
+ * place).  x_dtype must be MI355X_FP8_DTYPE_BF16 (fp16 returns MI355X_FP8_ERR_UNSUPPORTED).
+ */
+int mi355x_fp8_rmsnorm_quant(const void* x, int x_dtype, int64_t M, int64_t K, int64_t sxm,
+                             const void* residual, int64_t ldr, void* residual_out, int64_t ldro,
+                             const void* weight, float eps, void* y, int64_t ldy, uint8_t* q,
+                             int64_t ldq, int64_t kpad, float* s, int64_t s_sm, int64_t s_sk,
+                             void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -70,6 +70,25 @@ int mi355x_fp8_silu_mul_quant(const void* gate, const void* up, int x_dtype, int
                                s_sk, static_cast<hipStream_t>(stream));
 }
 
+int mi355x_fp8_rmsnorm_quant(const void* x, int x_dtype, int64_t M, int64_t K, int64_t sxm,
+                             const void* residual, int64_t ldr, void* residual_out, int64_t ldro,
+                             const void* weight, float eps, void* y, int64_t ldy, uint8_t* q,
+                             int64_t ldq, int64_t kpad, float* s, int64_t s_sm, int64_t s_sk,
+                             void* stream) {
+  if (!valid_dtype(x_dtype) || M < 0 || K < 128 || K % 4 != 0 || sxm < K || kpad < K ||
+      kpad > cdiv64(K, 128) * 128 || ldq < kpad || (y != nullptr && ldy < K) ||
+      (residual != nullptr && (ldr < K || residual_out == nullptr || ldro < K)))
+    return MI355X_FP8_ERR_INVALID;
+  // bf16 only: the reference fuses the norm for bf16 activations (fused.py:265-267).
+  if (x_dtype != MI355X_FP8_DTYPE_BF16) return MI355X_FP8_ERR_UNSUPPORTED;
+  if (M == 0) return MI355X_FP8_OK;
+  if (!x || !weight || !q || !s) return MI355X_FP8_ERR_INVALID;
+  return launch_rmsnorm_quant(static_cast<const uint16_t*>(x), sxm, static_cast<const uint16_t*>(residual), ldr,
+                              static_cast<uint16_t*>(residual_out), ldro, static_cast<const uint16_t*>(weight), eps, M,
+                              K, static_cast<uint16_t*>(y), ldy, q, ldq, kpad, s, s_sm, s_sk,
+                              static_cast<hipStream_t>(stream));
+}
+
 size_t mi355x_fp8_block_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int config) {
   GemmPlan plan;
   if (plan_gemm(M, N, K, config, &plan) != MI355X_FP8_OK) return 0;

@@ -44,21 +44,8 @@ __global__ __launch_bounds__(kQuantThreads) void act_quant_kernel(
     for (int i = 0; i < 8; ++i) t[i] = (live && k0 + i < K) ? to_f32(x[m * sxm + (k0 + i) * sxk]) : 0.0f;
   }
 
-  float amax = 0.0f;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(t[i]));
-#pragma unroll
-  for (int off = 8; off >= 1; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 16));
-
-  const float scale = amax / 448.0f;
-  const float den = scale > 1e-12f ? scale : 1e-12f;
   uint32_t packed[2];
-#pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const uint32_t lo = cvt_pk_e4m3(t[4 * i] / den, t[4 * i + 1] / den);
-    const uint32_t hi = cvt_pk_e4m3(t[4 * i + 2] / den, t[4 * i + 3] / den);
-    packed[i] = lo | (hi << 16);
-  }
+  const float scale = quant_group16(t, packed);
   if (!live) return;
   if (vec_out && k0 + 8 <= kpad) {
     *reinterpret_cast<uint2*>(q + m * ldq + k0) = make_uint2(packed[0], packed[1]);

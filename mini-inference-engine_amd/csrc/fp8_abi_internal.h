@@ -17,6 +17,13 @@ int launch_silu_mul_quant(const void* gate, const void* up, int dtype, int64_t l
                           uint16_t* h_out, int64_t ldh, uint8_t* q, int64_t ldq, int64_t kpad, float* s,
                           int64_t ssm, int64_t ssk, hipStream_t stream);
 
+int launch_rmsnorm_quant(const uint16_t* x, int64_t sxm, const uint16_t* res, int64_t ldr, uint16_t* res_out,
+                         int64_t ldro, const uint16_t* weight, float eps, int64_t M, int64_t K, uint16_t* y,
+                         int64_t ldy, uint8_t* q, int64_t ldq, int64_t kpad, float* s, int64_t ssm, int64_t ssk,
+                         hipStream_t stream);
+// Virtual threads per row of PyTorch's last-dim reduction (the RMSNorm summation order).
+int rmsnorm_block_width(int64_t rows, int64_t K);
+
 // Plan of one block-GEMM launch: which kernel and its tile shape.
 struct GemmPlan {
   int kernel;       // MI355X_FP8_CONFIG_STREAM or MI355X_FP8_CONFIG_TILE128

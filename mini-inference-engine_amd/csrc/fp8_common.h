@@ -50,9 +50,35 @@ template <> struct OutCvt<f16_t> {
   __device__ static uint16_t cvt(float f) { return f32_to_f16_bits(f); }
 };
 
+// fp32 rounded to the nearest bf16 (ties to even), returned as fp32.
+__device__ __forceinline__ float round_bf16(float f) {
+  return __uint_as_float(static_cast<uint32_t>(f32_to_bf16_bits(f)) << 16);
+}
+
 // Two fp32 -> two OCP e4m3fn codes (round-to-nearest-even), packed into the low 16 bits.
 __device__ __forceinline__ uint32_t cvt_pk_e4m3(float a, float b) {
   return static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false)) & 0xffffu;
+}
+
+// The quantizer of one 128-wide group held by a 16-lane slice, 8 consecutive elements per
+// lane (reference engine/kernels/sm89_fp8.py:321-324): scale = amax / 448 (IEEE division,
+// stored raw), codes = e4m3fn(t / max(scale, 1e-12)), round-to-nearest-even, saturating.
+// Returns the scale (the same in all 16 lanes); packed[0..1] receive this lane's 8 codes.
+__device__ __forceinline__ float quant_group16(const float (&t)[8], uint32_t (&packed)[2]) {
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(t[i]));
+#pragma unroll
+  for (int off = 8; off >= 1; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 16));
+  const float scale = amax / 448.0f;
+  const float den = scale > 1e-12f ? scale : 1e-12f;
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const uint32_t lo = cvt_pk_e4m3(t[4 * i] / den, t[4 * i + 1] / den);
+    const uint32_t hi = cvt_pk_e4m3(t[4 * i + 2] / den, t[4 * i + 3] / den);
+    packed[i] = lo | (hi << 16);
+  }
+  return scale;
 }
 
 // D(16x16, fp32) = A(16 x 128 e4m3) * B(128 x 16 e4m3), accumulator input zero.

@@ -21,10 +21,6 @@ namespace {
 constexpr int kSmqThreads = 256;
 constexpr int kSmqUnits = kSmqThreads / 16;
 
-__device__ __forceinline__ float round_bf16(float f) {
-  return __uint_as_float(static_cast<uint32_t>(f32_to_bf16_bits(f)) << 16);
-}
-
 template <typename InT>
 __global__ __launch_bounds__(kSmqThreads) void silu_mul_quant_kernel(
     const InT* __restrict__ gate, const InT* __restrict__ up, int64_t ld, int64_t M, int64_t I,
@@ -60,25 +56,14 @@ __global__ __launch_bounds__(kSmqThreads) void silu_mul_quant_kernel(
 
   float t[8];
   uint16_t hb[8];
-  float amax = 0.0f;
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     const float silu = round_bf16(gv[i] / (1.0f + expf(-gv[i])));
     hb[i] = f32_to_bf16_bits(silu * uv[i]);
     t[i] = __uint_as_float(static_cast<uint32_t>(hb[i]) << 16);
-    amax = fmaxf(amax, fabsf(t[i]));
   }
-#pragma unroll
-  for (int off = 8; off >= 1; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 16));
-  const float scale = amax / 448.0f;
-  const float den = scale > 1e-12f ? scale : 1e-12f;
   uint32_t packed[2];
-#pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const uint32_t lo = cvt_pk_e4m3(t[4 * i] / den, t[4 * i + 1] / den);
-    const uint32_t hi = cvt_pk_e4m3(t[4 * i + 2] / den, t[4 * i + 3] / den);
-    packed[i] = lo | (hi << 16);
-  }
+  const float scale = quant_group16(t, packed);
   if (!live) return;
   if (vec && k0 + 8 <= kpad) {
     *reinterpret_cast<uint2*>(q + m * ldq + k0) = make_uint2(packed[0], packed[1]);

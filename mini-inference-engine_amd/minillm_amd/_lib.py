@@ -42,6 +42,8 @@ EXPORTS = {
                                _i64, _i64, _i64, _ptr, _size, _int, _ptr], _int),
     "mi355x_fp8_silu_mul_quant": ([_ptr, _ptr, _int, _i64, _i64, _i64, _ptr, _i64, _ptr, _i64, _i64, _ptr, _i64, _i64,
                                    _ptr], _int),
+    "mi355x_fp8_rmsnorm_quant": ([_ptr, _int, _i64, _i64, _i64, _ptr, _i64, _ptr, _i64, _ptr, ctypes.c_float, _ptr,
+                                  _i64, _ptr, _i64, _i64, _ptr, _i64, _i64, _ptr], _int),
     "mi355x_fp8_linear_workspace_bytes": ([_i64, _i64, _i64, _int], _size),
     "mi355x_fp8_linear": ([_ptr, _int, _i64, _i64, _i64, _i64, _ptr, _i64, _ptr, _i64, _i64, _i64, _ptr, _int,
                            _i64, _ptr, _size, _int, _ptr], _int),

@@ -410,6 +410,94 @@ def silu_mul_quant_mi355x_fp8(gate: torch.Tensor, up: torch.Tensor, *, scale_lay
     return q, s
 
 
+def _quant_outputs(m: int, k: int, device: torch.device, scale_layout: str):
+    groups = (k + 127) // 128
+    q = torch.empty((m, k), device=device, dtype=torch.float8_e4m3fn)
+    if scale_layout == "row":
+        s = torch.empty((m, groups), device=device, dtype=torch.float32)
+        return q, s, groups, 1
+    mpad = max(64, -(-m // 64) * 64)
+    s = torch.empty((groups, mpad), device=device, dtype=torch.float32)[:, :m].t()
+    return q, s, 1, mpad
+
+
+def rmsnorm_quant_mi355x_fp8(x: torch.Tensor, weight: torch.Tensor, eps: float,
+                             residual: torch.Tensor | None = None, *, scale_layout: str = "kgroup",
+                             return_intermediate: bool = False):
+    """Qwen3 RMSNorm (optionally after the residual add), quantized per row and 128-column
+    group, in one kernel: the input side of the q/k/v and gate/up projections.
+
+    The norm is the reference's rms_norm (engine/kernels/fused.py:89-124, 165-199):
+    ``y = bf16(weight * bf16(x * rsqrt(mean(x^2) + eps)))``, with the row sum in PyTorch's
+    reduction order and, with ``residual``, ``x`` replaced by ``bf16(x + residual)``.  The
+    reciprocal square root is correctly rounded here (the reference's is libdevice's
+    approximation), so y can differ from the reference in the last bf16 place.  The
+    quantization is the activation quantizer's (sm89_fp8.py:304-332) applied to y.
+
+    Returns ``(q, s)``, plus the residual sum ``bf16(x + residual)`` when ``residual`` is
+    given; with ``return_intermediate`` the bf16 ``y`` comes first.
+    """
+
+    if x.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16:
+        raise ValueError("rmsnorm_quant takes bf16 activations and a bf16 norm weight")
+    if scale_layout not in {"row", "kgroup"}:
+        raise ValueError(f"Unknown scale layout: {scale_layout!r}")
+    if not x.is_cuda or not mi355x_available(x.device):
+        raise RuntimeError("rmsnorm_quant requires an MI355X (gfx950) GPU")
+    k = int(x.shape[-1])
+    if k % 4 or k < 128:
+        raise ValueError("rms_norm reproduces PyTorch's vectorized reduction: width must be a multiple of 4, >= 128")
+    if tuple(weight.shape) != (k,):
+        raise ValueError("norm weight must have shape (width,)")
+    x2 = x.reshape(-1, k)
+    if x2.stride(-1) != 1:
+        x2 = x2.contiguous()
+    w1 = weight.contiguous()
+    m = x2.shape[0]
+    r2 = summed = None
+    if residual is not None:
+        if residual.shape != x.shape or residual.dtype != torch.bfloat16:
+            raise ValueError("residual must be bf16 with the shape of x")
+        r2 = residual.reshape(-1, k)
+        if r2.stride(-1) != 1:
+            r2 = r2.contiguous()
+        summed = torch.empty((m, k), device=x.device, dtype=torch.bfloat16)
+    q, s, s_sm, s_sk = _quant_outputs(m, k, x.device, scale_layout)
+    y = torch.empty((m, k), device=x.device, dtype=torch.bfloat16) if return_intermediate else None
+    if m:
+        _lib.check(_lib.load().mi355x_fp8_rmsnorm_quant(
+            x2.data_ptr(), _lib.DTYPE_BF16, m, k, x2.stride(0),
+            None if r2 is None else r2.data_ptr(), 0 if r2 is None else r2.stride(0),
+            None if summed is None else summed.data_ptr(), k, w1.data_ptr(), float(eps),
+            None if y is None else y.data_ptr(), k, q.data_ptr(), k, k, s.data_ptr(), s_sm, s_sk,
+            _stream_ptr(x.device)))
+    shape = tuple(x.shape)
+    out = [q.reshape(shape), s]
+    if summed is not None:
+        out.append(summed.reshape(shape))
+    if y is not None:
+        out.insert(0, y.reshape(shape))
+    return tuple(out)
+
+
+def rmsnorm_linear_mi355x_fp8(x: torch.Tensor, norm_weight: torch.Tensor, eps: float, weight: torch.Tensor,
+                              weight_scale_inv: torch.Tensor, residual: torch.Tensor | None = None,
+                              output_dtype: torch.dtype | None = None):
+    """``fp8_linear(rms_norm(x [+ residual]), weight)`` with the norm and the activation
+    quantizer fused into one kernel (the q/k/v or gate/up projection of a Qwen3 layer).
+    Returns the projection, plus the residual sum when ``residual`` is given."""
+
+    outs = rmsnorm_quant_mi355x_fp8(x, norm_weight, eps, residual)
+    q, s = outs[0], outs[1]
+    k = int(x.shape[-1])
+    n = int(weight.shape[0])
+    out_dtype = output_dtype or torch.bfloat16
+    out = torch.empty((q.numel() // k, n), device=x.device, dtype=out_dtype)
+    launch_block_gemm(q.reshape(-1, k), weight, out, s, weight_scale_inv)
+    out = out.reshape(*x.shape[:-1], n)
+    return (out, outs[2]) if residual is not None else out
+
+
 def mlp_forward_mi355x_fp8(x: torch.Tensor, gate_up_weight: torch.Tensor, gate_up_scale: torch.Tensor,
                            down_weight: torch.Tensor, down_scale: torch.Tensor,
                            output_dtype: torch.dtype | None = None) -> torch.Tensor:

@@ -21,6 +21,7 @@
  *     brute-force pure-Python evaluation on tiny tail shapes.
  */
 #include <math.h>
+#include <stdlib.h>
 #include <stdint.h>
 #include <string.h>
 #ifdef _OPENMP
@@ -229,6 +230,75 @@ void orc_silu_mul(const uint16_t* gate, const uint16_t* up, int64_t n, uint16_t*
     float silu = orc_bf16_to_f32(orc_f32_to_bf16(g / den));
     h[i] = orc_f32_to_bf16(silu * u);
   }
+}
+
+/* Threads PyTorch's CUDA reduction assigns to one row of a last-dim fp32 mean over 4-wide
+ * vectors (setReduceConfig), as the reference reproduces it in _torch_reduce_block_width
+ * (engine/kernels/fused.py:205-214). */
+static int64_t orc_last_pow2(int64_t n) {
+  int64_t p = 1;
+  while (p * 2 <= n) p *= 2;
+  return p;
+}
+int64_t orc_rmsnorm_block_width(int64_t rows, int64_t n_cols) {
+  const int64_t max_threads = 512, warp = 32;
+  int64_t dim0 = n_cols / 4;
+  int64_t dim0_pow2 = dim0 < max_threads ? orc_last_pow2(dim0) : max_threads;
+  int64_t dim1_pow2 = rows < max_threads ? orc_last_pow2(rows > 0 ? rows : 1) : max_threads;
+  int64_t lim = max_threads / (dim0_pow2 < warp ? dim0_pow2 : warp);
+  int64_t height = dim1_pow2 < lim ? dim1_pow2 : lim;
+  int64_t cap = max_threads / height;
+  return dim0_pow2 < cap ? dim0_pow2 : cap;
+}
+
+/* Qwen3 RMSNorm as the reference's _rms_norm_kernel computes it (engine/kernels/fused.py:
+ * 89-124, 165-199) for `rows` rows of width n_cols (a multiple of 4):
+ *   x   = bf16(x + residual)               with a residual (summed[] receives it)
+ *   ss  = rounded squares summed in PyTorch's order: bw = orc_rmsnorm_block_width(rows, K)
+ *         threads; thread t runs four accumulators over vectors v = k*bw + t (element 4v+q
+ *         into accumulator q), combines ((a0 + a1) + a2) + a3; threads fold s[t] += s[t+h]
+ *         for h = bw/2 .. 1
+ *   var = ss * fl(1 / K);  inv = 1 / sqrt(var + eps)  (double, rounded once to fp32 -- the
+ *         reference uses libdevice's approximate rsqrt here)
+ *   y   = bf16(w * bf16(x * inv))
+ * x and residual rows are `ld` elements apart; y and summed are dense. */
+void orc_rmsnorm(const uint16_t* x, const uint16_t* residual, int64_t ld, const uint16_t* w, int64_t rows,
+                 int64_t n_cols, float eps, uint16_t* y, uint16_t* summed) {
+  const int64_t bw = orc_rmsnorm_block_width(rows, n_cols);
+  const int64_t nvec = n_cols / 4;
+  const float inv_k = 1.0f / (float)n_cols;
+  float* part = (float*)malloc((size_t)bw * sizeof(float));
+  float* xs = (float*)malloc((size_t)n_cols * sizeof(float));
+  for (int64_t r = 0; r < rows; ++r) {
+    for (int64_t c = 0; c < n_cols; ++c) {
+      float v = orc_bf16_to_f32(x[r * ld + c]);
+      if (residual) {
+        uint16_t sb = orc_f32_to_bf16(v + orc_bf16_to_f32(residual[r * ld + c]));
+        summed[r * n_cols + c] = sb;
+        v = orc_bf16_to_f32(sb);
+      }
+      xs[c] = v;
+    }
+    for (int64_t t = 0; t < bw; ++t) {
+      float a[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+      for (int64_t v = t; v < nvec; v += bw)
+        for (int q = 0; q < 4; ++q) {
+          float sq = xs[4 * v + q] * xs[4 * v + q];
+          a[q] = a[q] + sq;
+        }
+      part[t] = ((a[0] + a[1]) + a[2]) + a[3];
+    }
+    for (int64_t h = bw / 2; h >= 1; h /= 2)
+      for (int64_t t = 0; t < h; ++t) part[t] = part[t] + part[t + h];
+    float var = part[0] * inv_k;
+    float inv = (float)(1.0 / sqrt((double)(var + eps)));
+    for (int64_t c = 0; c < n_cols; ++c) {
+      float normed = orc_bf16_to_f32(orc_f32_to_bf16(xs[c] * inv));
+      y[r * n_cols + c] = orc_f32_to_bf16(orc_bf16_to_f32(w[c]) * normed);
+    }
+  }
+  free(part);
+  free(xs);
 }
 
 int orc_max_threads(void) {

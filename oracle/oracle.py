@@ -54,6 +54,9 @@ def lib():
             _ptr, _ptr, ctypes.c_int]
         handle.orc_max_threads.restype = ctypes.c_int
         handle.orc_silu_mul.argtypes = [_ptr, _ptr, _i64, _ptr]
+        handle.orc_rmsnorm_block_width.argtypes = [_i64, _i64]
+        handle.orc_rmsnorm_block_width.restype = _i64
+        handle.orc_rmsnorm.argtypes = [_ptr, _ptr, _i64, _ptr, _i64, _i64, ctypes.c_float, _ptr, _ptr]
         _lib = handle
     return _lib
 
@@ -149,6 +152,34 @@ def silu_mul(gate_bits: np.ndarray, up_bits: np.ndarray) -> np.ndarray:
     out = np.empty(g.shape, dtype=np.uint16)
     lib().orc_silu_mul(_p(g), _p(u), g.size, _p(out))
     return out
+
+
+def rmsnorm_block_width(rows: int, n_cols: int) -> int:
+    return int(lib().orc_rmsnorm_block_width(rows, n_cols))
+
+
+def rmsnorm(x_bits: np.ndarray, w_bits: np.ndarray, eps: float,
+            residual_bits: np.ndarray | None = None) -> tuple[np.ndarray, np.ndarray | None]:
+    """Qwen3 RMSNorm in the reference's arithmetic and summation order
+    (engine/kernels/fused.py:89-124, 165-199), bf16 bits in and out.  Returns ``(y, summed)``;
+    ``summed`` (bf16(x + residual)) is None without a residual."""
+
+    x = np.ascontiguousarray(x_bits, dtype=np.uint16)
+    w = np.ascontiguousarray(w_bits, dtype=np.uint16)
+    rows, n_cols = x.shape
+    if n_cols % 4 or w.shape != (n_cols,):
+        raise ValueError("width must be a multiple of 4 and match the weight")
+    y = np.empty((rows, n_cols), dtype=np.uint16)
+    summed = None
+    r = None
+    if residual_bits is not None:
+        r = np.ascontiguousarray(residual_bits, dtype=np.uint16)
+        if r.shape != x.shape:
+            raise ValueError("shape mismatch")
+        summed = np.empty((rows, n_cols), dtype=np.uint16)
+    lib().orc_rmsnorm(_p(x), None if r is None else _p(r), n_cols, _p(w), rows, n_cols, float(eps), _p(y),
+                      None if summed is None else _p(summed))
+    return y, summed
 
 
 def max_threads() -> int:

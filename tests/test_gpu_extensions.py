@@ -140,3 +140,59 @@ def test_checkpoint_loader_feeds_the_linear(gpu, tmp_path):
         part = fp8.mi355x_fp8_linear(x.to(gpu), wp, sp, [128, 128])
         assert bitwise_equal(part, out[:, row:row + wp.shape[0]].contiguous())
         row += wp.shape[0]
+
+
+@pytest.mark.parametrize("rows,width", [(1, 2560), (2, 2560), (4, 2560), (8, 2560), (16, 2560), (300, 2560),
+                                        (3, 260), (64, 128), (5, 4096)])
+@pytest.mark.parametrize("with_residual", [False, True])
+def test_rmsnorm_quant_matches_oracle(gpu, rows, width, with_residual):
+    """The fused RMSNorm + quantizer against the oracle: y and the residual sum bitwise (same
+    summation order, same correctly rounded 1/sqrt), codes and scales bit-exact."""
+
+    _note("rmsnorm_quant", rows, width, with_residual)
+    gen = torch.Generator().manual_seed(rows * 31 + width)
+    x = (torch.randn(rows, width, generator=gen) * 2).to(torch.bfloat16)
+    x[0, :4] = torch.tensor([0.0, -0.0, 200.0, -3.0e-3]).to(torch.bfloat16)
+    r = torch.randn(rows, width, generator=gen).to(torch.bfloat16) if with_residual else None
+    w = (torch.rand(width, generator=gen) + 0.5).to(torch.bfloat16)
+    outs = fp8.rmsnorm_quant_mi355x_fp8(x.to(gpu), w.to(gpu), 1e-6, None if r is None else r.to(gpu),
+                                        scale_layout="row", return_intermediate=True)
+    y, q, s = outs[0], outs[1], outs[2]
+    y_ref, summed_ref = oracle.rmsnorm(bits16(x), bits16(w), 1e-6, None if r is None else bits16(r))
+    assert np.array_equal(bits16(y), y_ref)
+    if with_residual:
+        assert np.array_equal(bits16(outs[3]), summed_ref)
+    q_ref, s_ref = oracle.act_quant(y_ref)
+    assert np.array_equal(codes(q), q_ref)
+    assert np.array_equal(s.cpu().numpy().view(np.uint32), s_ref.view(np.uint32))
+    # K-group-major scales: same values.
+    outs2 = fp8.rmsnorm_quant_mi355x_fp8(x.to(gpu), w.to(gpu), 1e-6, None if r is None else r.to(gpu))
+    assert bitwise_equal(outs2[0], q)
+    assert np.array_equal(outs2[1].cpu().numpy().view(np.uint32), s.cpu().numpy().view(np.uint32))
+
+
+def test_rmsnorm_linear_equals_unfused(gpu):
+    """Norm + quantizer fused in front of the GEMM gives the same bits as the linear on the
+    normalized activations (one quantizer, one GEMM arithmetic)."""
+
+    gen = torch.Generator().manual_seed(3)
+    x = torch.randn(40, 2560, generator=gen).to(torch.bfloat16).to(gpu)
+    r = torch.randn(40, 2560, generator=gen).to(torch.bfloat16).to(gpu)
+    nw = (torch.rand(2560, generator=gen) + 0.5).to(torch.bfloat16).to(gpu)
+    w, ws = make_baseline_weights(ModelShape("qkv", 6144, 2560), SEED)
+    wg, wsg = w.to(gpu), ws.to(gpu)
+    out, summed = fp8.rmsnorm_linear_mi355x_fp8(x, nw, 1e-6, wg, wsg, residual=r)
+    y, _, _, summed2 = fp8.rmsnorm_quant_mi355x_fp8(x, nw, 1e-6, r, return_intermediate=True)
+    assert bitwise_equal(summed, summed2)
+    assert bitwise_equal(out, fp8.mi355x_fp8_linear(y, wg, wsg, [128, 128]))
+    assert_close_rows(out, oracle_linear(y.cpu(), w, ws))
+
+
+def test_rmsnorm_quant_rejects(gpu):
+    w = torch.ones(256, dtype=torch.bfloat16, device=gpu)
+    with pytest.raises(ValueError, match="bf16"):
+        fp8.rmsnorm_quant_mi355x_fp8(torch.zeros(2, 256, dtype=torch.float16, device=gpu), w, 1e-6)
+    with pytest.raises(ValueError, match="multiple of 4"):
+        fp8.rmsnorm_quant_mi355x_fp8(torch.zeros(2, 130, dtype=torch.bfloat16, device=gpu), w[:130], 1e-6)
+    with pytest.raises(ValueError, match="multiple of 4"):
+        fp8.rmsnorm_quant_mi355x_fp8(torch.zeros(2, 124, dtype=torch.bfloat16, device=gpu), w[:124], 1e-6)

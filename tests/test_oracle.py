@@ -204,3 +204,66 @@ def test_silu_mul_matches_torch_bf16_semantics():
     ref = bits16(torch.nn.functional.silu(g) * u)
     ulps = np.abs(ours.astype(np.int32) - ref.astype(np.int32))
     assert ulps.max() <= 1 and (ulps == 0).mean() > 0.99
+
+
+# ---- RMSNorm (reference engine/kernels/fused.py:89-124, 165-214) -------------------------
+
+def test_rmsnorm_block_width_known_values():
+    """The reference's _torch_reduce_block_width at the widths Qwen3 uses (worked by hand
+    from its formula: dim0 = width / 4 vectors, 512-thread blocks, 32-wide warps)."""
+
+    for rows, width, bw in [(1, 2560, 512), (2, 2560, 256), (4, 2560, 128), (8, 2560, 64), (16, 2560, 32),
+                            (2048, 2560, 32), (1, 128, 32), (64, 128, 32), (1, 256, 64), (3, 1024, 256)]:
+        assert oracle.rmsnorm_block_width(rows, width) == bw, (rows, width)
+
+
+def _bf16_bits(t):
+    return t.contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+def test_rmsnorm_closed_forms():
+    """Rows whose sum of squares is exact in any order: the result is then fixed by the
+    formula alone (y = bf16(w * bf16(x * fl(1/sqrt(var + eps)))))."""
+
+    eps = np.float32(1e-6)
+    for width in (128, 2560):
+        w = (torch.arange(width) % 7 * 0.25 + 0.5).to(torch.bfloat16)
+        for c in (2.0, -0.5, 3.0):
+            x = torch.full((3, width), c, dtype=torch.bfloat16)
+            y, _ = oracle.rmsnorm(_bf16_bits(x), _bf16_bits(w), float(eps))
+            ss = np.float32(c * c * width)                      # exact
+            var = np.float32(ss * np.float32(np.float32(1.0) / np.float32(width)))
+            inv = np.float32(1.0 / np.sqrt(np.float64(np.float32(var + eps))))
+            normed = torch.tensor(np.float32(c) * inv, dtype=torch.float32).to(torch.bfloat16).float()
+            expect = (w.float() * normed).to(torch.bfloat16)
+            assert np.array_equal(y[0], _bf16_bits(expect)) and np.array_equal(y[2], y[0])
+        # One non-zero element: ss = a^2 exactly.
+        x = torch.zeros(1, width, dtype=torch.bfloat16)
+        x[0, 5] = 12.0
+        y, _ = oracle.rmsnorm(_bf16_bits(x), _bf16_bits(w), float(eps))
+        var = np.float32(np.float32(144.0) * np.float32(np.float32(1.0) / np.float32(width)))
+        inv = np.float32(1.0 / np.sqrt(np.float64(np.float32(var + eps))))
+        normed = torch.tensor(np.float32(12.0) * inv).to(torch.bfloat16).float()
+        assert y[0, 5] == _bf16_bits((w[5].float() * normed).to(torch.bfloat16).reshape(1))[0]
+        assert (y[0, np.arange(width) != 5] & 0x7FFF).max() == 0   # zeros stay zero
+
+
+def test_rmsnorm_matches_torch_within_one_ulp_and_residual_sum_is_exact():
+    """Against torch's CPU Qwen3RMSNorm (its own summation order): within one bf16 ulp, and
+    bitwise almost everywhere; the residual add is bitwise torch's bf16 add."""
+
+    gen = torch.Generator().manual_seed(5)
+    eps = 1e-6
+    for rows, width in [(1, 2560), (8, 2560), (33, 2560), (4, 4096), (16, 132)]:
+        x = (torch.randn(rows, width, generator=gen) * 3).to(torch.bfloat16)
+        r = (torch.randn(rows, width, generator=gen)).to(torch.bfloat16)
+        w = (torch.rand(width, generator=gen) + 0.5).to(torch.bfloat16)
+        y, summed = oracle.rmsnorm(_bf16_bits(x), _bf16_bits(w), eps, _bf16_bits(r))
+        s_ref = x + r
+        assert np.array_equal(summed, _bf16_bits(s_ref))
+        h = s_ref.float()
+        ref = w * (h * torch.rsqrt(h.pow(2).mean(-1, keepdim=True) + eps)).to(torch.bfloat16)
+        diff = np.abs(y.astype(np.int32) - _bf16_bits(ref).astype(np.int32))
+        assert diff.max() <= 1 and (diff == 0).mean() > 0.99, (rows, width, diff.max(), (diff == 0).mean())
+    with pytest.raises(ValueError):
+        oracle.rmsnorm(np.zeros((2, 130), np.uint16), np.zeros(130, np.uint16), 1e-6)
