@@ -189,6 +189,7 @@ def main(argv=None) -> int:
     if not args.no_extras:
         print("timing MLP block and 36-layer stack", file=sys.stderr, flush=True)
         extras["mlp"] = bench_mlp(torch, fp8, stream, args, make_baseline_weights, make_baseline_activations)
+        extras["rmsnorm_quant"] = bench_rmsnorm_quant(torch, fp8, stream, args)
         extras["stack"] = bench_stack(torch, fp8, stream, args, make_baseline_weights, make_baseline_activations,
                                       projs)
 
@@ -231,6 +232,25 @@ def main(argv=None) -> int:
     }
     print(json.dumps(line), flush=True)
     return 0
+
+
+def bench_rmsnorm_quant(torch, fp8, stream, args):
+    """The fused residual add + RMSNorm + 1x128 quantizer in front of qkv / gate_up (hidden
+    2560), at the prefill and decode row counts; bytes = 2K x + 2K residual + 2K residual
+    sum + K codes + 4 K/128 scales per row."""
+
+    out = {}
+    gen = torch.Generator().manual_seed(SEED)
+    for m in (args.prefill_m, args.decode_m):
+        k = 2560
+        x = torch.randn(m, k, generator=gen).to(torch.bfloat16).cuda()
+        r = torch.randn(m, k, generator=gen).to(torch.bfloat16).cuda()
+        w = (torch.rand(k, generator=gen) + 0.5).to(torch.bfloat16).cuda()
+        ms = timed_graph(torch, stream, lambda: fp8.rmsnorm_quant_mi355x_fp8(x, w, 1e-6, r), 1, args.steps,
+                         args.warmup, args.eager)
+        nbytes = m * (6 * k + k + 4 * (k // 128))
+        out[f"m{m}"] = {"us": round(ms * 1e3, 2), "gbps": round(nbytes / (ms * 1e6), 1)}
+    return out
 
 
 def bench_mlp(torch, fp8, stream, args, make_w, make_x):

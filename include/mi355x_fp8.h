@@ -118,7 +118,9 @@ int mi355x_fp8_silu_mul_quant(const void* gate, const void* up, int x_dtype, int
  * the input of the q/k/v and gate/up projections.  Replaces rms_norm
  * (engine/kernels/fused.py:89-124, 165-199) plus the quantizer launch of the projection
  * that consumes its output (engine/kernels/sm89_fp8.py:401-424).
- *   x        : M x K bf16, (m, k) at x[m*sxm + k]; K % 4 == 0 and K >= 128
+ *   x        : M x K bf16, (m, k) at x[m*sxm + k]; K % 4 == 0 and K >= 128 (rows wider
+ *              than 16128 return MI355X_FP8_ERR_UNSUPPORTED: a row and the weight are
+ *              staged in LDS)
  *   residual : optional (NULL: none) M x K bf16 at residual[m*ldr + k]; then residual_out
  *              (m, k) at residual_out[m*ldro + k] receives bf16(x + residual), the input
  *              of the normalization

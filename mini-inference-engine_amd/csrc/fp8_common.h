@@ -29,10 +29,10 @@ __device__ __forceinline__ float to_f32(f16_t h) {
 
 // fp32 -> bf16 with round-to-nearest-even (NaN kept quiet).
 __device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return static_cast<uint16_t>(u >> 16);
+  const __bf16 v = static_cast<__bf16>(f);  // v_cvt_pk_bf16_f32: round to nearest even
+  uint16_t b;
+  __builtin_memcpy(&b, &v, 2);
+  return b;
 }
 // fp32 -> binary16 with the hardware's round-to-nearest-even conversion.
 __device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {

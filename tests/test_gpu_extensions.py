@@ -143,7 +143,8 @@ def test_checkpoint_loader_feeds_the_linear(gpu, tmp_path):
 
 
 @pytest.mark.parametrize("rows,width", [(1, 2560), (2, 2560), (4, 2560), (8, 2560), (16, 2560), (300, 2560),
-                                        (3, 260), (64, 128), (5, 4096)])
+                                        (3, 260), (64, 128), (5, 4096), (3, 16000), (1, 128), (256, 2560),
+                                        (257, 2560), (513, 2560), (200, 16000)])
 @pytest.mark.parametrize("with_residual", [False, True])
 def test_rmsnorm_quant_matches_oracle(gpu, rows, width, with_residual):
     """The fused RMSNorm + quantizer against the oracle: y and the residual sum bitwise (same
@@ -188,8 +189,24 @@ def test_rmsnorm_linear_equals_unfused(gpu):
     assert_close_rows(out, oracle_linear(y.cpu(), w, ws))
 
 
+def test_rmsnorm_quant_strided_rows(gpu):
+    """Rows with a padded stride (not a multiple of 8 elements: the unvectorized path) give
+    the same bits as contiguous rows."""
+
+    gen = torch.Generator().manual_seed(9)
+    base = torch.randn(6, 2563, generator=gen).to(torch.bfloat16).to(gpu)
+    x = base[:, :2560]
+    w = (torch.rand(2560, generator=gen) + 0.5).to(torch.bfloat16).to(gpu)
+    got = fp8.rmsnorm_quant_mi355x_fp8(x, w, 1e-6, return_intermediate=True)
+    ref = fp8.rmsnorm_quant_mi355x_fp8(x.contiguous(), w, 1e-6, return_intermediate=True)
+    assert bitwise_equal(got[0], ref[0]) and bitwise_equal(got[1], ref[1])
+
+
 def test_rmsnorm_quant_rejects(gpu):
     w = torch.ones(256, dtype=torch.bfloat16, device=gpu)
+    with pytest.raises(RuntimeError, match="unsupported"):
+        fp8.rmsnorm_quant_mi355x_fp8(torch.zeros(1, 16132, dtype=torch.bfloat16, device=gpu),
+                                     torch.ones(16132, dtype=torch.bfloat16, device=gpu), 1e-6)
     with pytest.raises(ValueError, match="bf16"):
         fp8.rmsnorm_quant_mi355x_fp8(torch.zeros(2, 256, dtype=torch.float16, device=gpu), w, 1e-6)
     with pytest.raises(ValueError, match="multiple of 4"):
