@@ -140,8 +140,8 @@ def main(argv=None) -> int:
     print(f"generating {sets} weight sets of {layer_bytes / 2**20:.1f} MiB", file=sys.stderr, flush=True)
     weights = [[make_baseline_weights(p, SEED + 1000 * s, device="cuda") for p in projs] for s in range(sets)]
 
-    def run_phase(m, outliers):
-        per_launch, quant = [], []
+    def run_phase(m, outliers, full_linear):
+        per_launch, quant, linear = [], [], []
         for i, p in enumerate(projs):
             x = make_baseline_activations(m, p.k, SEED, outliers=outliers, device="cuda")
             q, s = fp8.quantize_mi355x_fp8_activation(x, scale_layout="kgroup")
@@ -155,16 +155,22 @@ def main(argv=None) -> int:
                 for _ in range(sets):
                     fp8.quantize_mi355x_fp8_activation(x, scale_layout="kgroup")
 
+            def linears(i=i, x=x):
+                for r in range(sets):
+                    fp8.mi355x_fp8_linear(x, weights[r][i][0], weights[r][i][1], [128, 128])
+
             per_launch.append(timed_graph(torch, stream, gemms, sets, args.steps, args.warmup, args.eager))
             quant.append(timed_graph(torch, stream, quants, sets, args.steps, args.warmup, args.eager))
-        return per_launch, quant
+            if full_linear:
+                linear.append(timed_graph(torch, stream, linears, sets, args.steps, args.warmup, args.eager))
+        return per_launch, quant, linear
 
     results = {}
     for phase, m, outliers in (("prefill", args.prefill_m, True), ("decode", args.decode_m, False)):
         if args.only and phase != args.only:
             continue
         print(f"timing {phase} M={m}", file=sys.stderr, flush=True)
-        mean, quant_ms = run_phase(m, outliers)
+        mean, quant_ms, linear_ms = run_phase(m, outliers, full_linear=phase == "decode")
         flops = [linear_flops(m, p.n, p.k) for p in projs]
         nbytes = [gemm_bytes(m, p.n, p.k) for p in projs]
         results[phase] = {
@@ -179,6 +185,14 @@ def main(argv=None) -> int:
             "quant": {p.name: {"us": 1e3 * quant_ms[i], "gbps": quant_bytes(m, p.k) / (quant_ms[i] * 1e6)}
                       for i, p in enumerate(projs)},
         }
+        if linear_ms:
+            # The whole linear from bf16 activations (quantization included), as a model calls
+            # it; same algorithmic bytes (gemm_bytes counts the activations as bf16).
+            lbytes = nbytes
+            results[phase]["linear"] = {
+                "step_ms": sum(linear_ms), "gbps": sum(lbytes) / (sum(linear_ms) * 1e6),
+                "per_proj": {p.name: {"us": 1e3 * linear_ms[i], "gbps": lbytes[i] / (linear_ms[i] * 1e6)}
+                             for i, p in enumerate(projs)}}
     if args.only:
         print(json.dumps({"phase": args.only, "detail": results}), flush=True)
         return 0
@@ -219,7 +233,9 @@ def main(argv=None) -> int:
                                "(value) and decode M=8 (decode.gbps); GEMM on pre-quantized activations",
                    "prefill_m": pre["m"], "decode_m": dec["m"], "weight_sets": sets},
         "decode": {"gbps": round(dec["gbps"], 1), "ms_per_step": round(dec["step_ms"], 4),
-                   "frac_of_hbm": round(dec["gbps"] / PEAK_HBM_GBPS, 4)},
+                   "frac_of_hbm": round(dec["gbps"] / PEAK_HBM_GBPS, 4),
+                   "linear_gbps": round(dec["linear"]["gbps"], 1),
+                   "linear_ms_per_step": round(dec["linear"]["step_ms"], 4)},
         "roofline": {"bound": "mfma", "kernel": "prefill block GEMM (M=2048, mean over the 4 projections)",
                      "achieved": round(pre["tflops"], 2), "peak": PEAK_FP8_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(pre["tflops"] / PEAK_FP8_TFLOPS, 4), "traffic": traffic_per_launch("prefill")},

@@ -85,6 +85,45 @@ def test_quantizer_subnormal_and_rounding_midpoints(gpu):
     assert bitwise_equal(s.cpu(), s_ref), bit_mismatch_details(s.cpu(), s_ref)
 
 
+def _division_sweep_groups(dtype, seed):
+    """One 128-wide group per positive finite amax of the format: amax, -amax, +-0 and 124
+    values drawn uniformly from [-amax, amax] and rounded to the format (so every group
+    exercises the scale division and the 128 element quotients under its own amax)."""
+
+    bits = torch.arange(1, 0x7F80 if dtype == torch.bfloat16 else 0x7C00, dtype=torch.int32)
+    amax = bits.to(torch.int16).view(dtype).float()
+    gen = torch.Generator().manual_seed(seed)
+    frac = torch.rand(amax.numel(), 124, generator=gen, dtype=torch.float64) * 2 - 1
+    body = (frac * amax.double()[:, None]).to(dtype).float()
+    body = torch.maximum(torch.minimum(body, amax[:, None]), -amax[:, None])  # rounding may step past amax
+    groups = torch.cat([amax[:, None], -amax[:, None], torch.zeros_like(amax)[:, None],
+                        -torch.zeros_like(amax)[:, None], body], dim=1)
+    return groups.to(dtype)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_quantizer_division_sweep(gpu, dtype):
+    """The quantizer's division by the scale against the oracle's IEEE division: every
+    positive finite amax of the format (one group each), and every value of the format
+    for a few amax values (1, 448, one where the 1e-12 clamp applies, the format's max)."""
+
+    _note("division sweep", dtype)
+    x = _division_sweep_groups(dtype, 3)
+    allv = torch.arange(-32768, 32768, dtype=torch.int32).to(torch.int16).view(dtype).float()
+    allv = allv[torch.isfinite(allv)]
+    top = 3.3895313892515355e38 if dtype == torch.bfloat16 else 65504.0
+    for amax in (1.0, 448.0, 1e-10, top):
+        a = torch.tensor(amax, dtype=dtype).float()
+        vals = allv[allv.abs() <= a]
+        pad = (-vals.numel()) % 127
+        vals = torch.cat([vals, torch.zeros(pad)]).reshape(-1, 127)
+        x = torch.cat([x, torch.cat([a.expand(vals.shape[0], 1), vals], dim=1).to(dtype)])
+    q, s = fp8.quantize_mi355x_fp8_activation(x.to(gpu))
+    q_ref, s_ref = oracle_quant(x)
+    assert bitwise_equal(q.cpu(), q_ref), bit_mismatch_details(q.cpu(), q_ref)
+    assert bitwise_equal(s.cpu(), s_ref), bit_mismatch_details(s.cpu(), s_ref)
+
+
 @pytest.mark.parametrize("shape", TAIL_SHAPES + (ModelShape("kv", 1024, 2560), ModelShape("o", 2560, 4096)),
                          ids=lambda s: s.name)
 @pytest.mark.parametrize("rows", [1, 7, 64, 65, 129, 300])
@@ -273,3 +312,31 @@ def test_prefill_tile_widths(gpu, rows, n, k):
     reg = torch.empty_like(out)
     fp8.launch_block_gemm(q, wg, reg, s_row, wsg)
     assert bitwise_equal(reg, out), bit_mismatch_details(reg, out)
+
+
+@pytest.mark.parametrize("shape", [ModelShape("kv", 1024, 2560), ModelShape("k264", 193, 264),
+                                   ModelShape("k200", 321, 200), ModelShape("k259", 129, 259),
+                                   ModelShape("down", 2560, 9728)], ids=lambda s: s.name)
+@pytest.mark.parametrize("rows", [1, 8, 16, 17, 32, 33, 64])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_decode_linear_equals_quantizer_then_gemm(gpu, shape, rows, dtype):
+    """The linear entry at decode sizes (contiguous and padded-stride rows, bf16 and fp16,
+    K tails) gives the bits of the activation quantizer followed by the stream GEMM."""
+
+    _note("decode linear", shape.name, rows, dtype)
+    x = make_activations(rows, shape.k, 11 + rows, dtype)
+    x[0, : min(8, shape.k)] = 0.0  # an all-zero chunk in the first group
+    w, ws = make_weights(shape, 5)
+    xg, wg, wsg = x.to(gpu), w.to(gpu), ws.to(gpu)
+    got = fp8.mi355x_fp8_linear(xg, wg, wsg, BLOCK)
+    q, s = fp8.quantize_mi355x_fp8_activation(xg)
+    ref = torch.empty_like(got)
+    fp8.launch_block_gemm(q, wg, ref, s, wsg, config=fp8.GEMM_CONFIGS[0])
+    assert bitwise_equal(got, ref), bit_mismatch_details(got, ref)
+    if dtype == torch.bfloat16:  # fp16 output overflows on the generator's huge row
+        assert_close_rows(got, oracle_linear(x, w, ws))
+    # A padded row stride that is not a multiple of 8 elements (the quantizer's scalar loads).
+    padded = torch.zeros(rows, shape.k + 3, dtype=dtype)
+    padded[:, : shape.k] = x
+    got2 = fp8.mi355x_fp8_linear(padded.to(gpu)[:, : shape.k], wg, wsg, BLOCK)
+    assert bitwise_equal(got2, ref), bit_mismatch_details(got2, ref)
