@@ -33,6 +33,12 @@ namespace mi355x {
 namespace {
 
 constexpr int kDmaThreads = 256;
+#ifndef MI355X_DMA_STAGES_FEW
+#define MI355X_DMA_STAGES_FEW 3  // ring depth when the tiles do not exceed the CUs
+#endif
+#ifndef MI355X_DMA_STAGES_MANY
+#define MI355X_DMA_STAGES_MANY 2  // ring depth otherwise (two workgroups per CU)
+#endif
 constexpr int kTileRows = 128;                          // activation rows per tile
 constexpr int kMaxBN = 160;                             // widest W tile (columns of the output tile)
 constexpr int kStageChunks = (kMaxBN + kTileRows) * 8 + 64;  // W tile, X tile, 4 x 64 scales (uint4 units)
@@ -50,6 +56,7 @@ struct DmaGeo {
 __shared__ uint4 stage0[kStageChunks];
 __shared__ uint4 stage1[kStageChunks];
 __shared__ uint4 stage2[kStageChunks];
+__shared__ uint4 stage3[kStageChunks];
 
 typedef __attribute__((address_space(3))) void lds_void_t;
 typedef const __attribute__((address_space(1))) void global_void_t;
@@ -63,11 +70,11 @@ __device__ __forceinline__ void dma4(const void* src, void* lds_dst) {
                                    (lds_void_t*)(lds_dst), 4, 0, 0);
 }
 
-// s_waitcnt with vmcnt = N (N <= 15) and lgkmcnt = 0, expcnt left at its maximum.
+// s_waitcnt with vmcnt = N (6 bits: 3:0 and 15:14) and lgkmcnt = 0, expcnt left at its maximum.
 template <int N>
 __device__ __forceinline__ void wait_vm_lgkm0() {
-  static_assert(N >= 0 && N < 16, "vmcnt immediate");
-  __builtin_amdgcn_s_waitcnt((N & 0xF) | (0x7 << 4));
+  static_assert(N >= 0 && N < 64, "vmcnt immediate");
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4));
 }
 
 __device__ __forceinline__ void tile_of_dma(int64_t pid, int64_t tiles_m, int64_t tiles_n, int64_t* tm,
@@ -99,7 +106,8 @@ template <int S>
 __device__ __forceinline__ uint4* stage_ptr() {
   if constexpr (S == 0) return stage0;
   else if constexpr (S == 1) return stage1;
-  else return stage2;
+  else if constexpr (S == 2) return stage2;
+  else return stage3;
 }
 
 template <int BN, int S>
@@ -174,7 +182,7 @@ __device__ __forceinline__ void k_step(v4f (&acc)[DmaGeo<BN>::kNI][4], const Dma
 }
 
 template <int STAGES, int BN, typename OutT>
-__global__ __launch_bounds__(kDmaThreads, 3 - STAGES + 1) void tile_gemm_dma_kernel(
+__global__ __launch_bounds__(kDmaThreads, STAGES == 2 ? 2 : 1) void tile_gemm_dma_kernel(
     const uint8_t* __restrict__ q, int64_t ldq, const float* __restrict__ as, int64_t as_sk,
     const uint8_t* __restrict__ w, int64_t ldw, const float* __restrict__ ws, int64_t ws_sn,
     int64_t ws_sk, uint16_t* __restrict__ out, int64_t ldo, int64_t M, int64_t N, int64_t KB,
@@ -231,12 +239,15 @@ __global__ __launch_bounds__(kDmaThreads, 3 - STAGES + 1) void tile_gemm_dma_ker
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
 
+  static_assert(STAGES >= 2 && STAGES <= 4, "stages");
   issue_stage<BN, 0>(src, 0, as_sk, wave, lane);
-  if constexpr (STAGES == 3) issue_stage<BN, 1>(src, KB > 1 ? 1 : 0, as_sk, wave, lane);
+  if constexpr (STAGES >= 3) issue_stage<BN, 1>(src, KB > 1 ? 1 : KB - 1, as_sk, wave, lane);
+  if constexpr (STAGES >= 4) issue_stage<BN, 2>(src, KB > 2 ? 2 : KB - 1, as_sk, wave, lane);
   for (int64_t kb = 0; kb < KB; kb += STAGES) {
     k_step<BN, STAGES, 0>(acc, src, kb, KB, as_sk, ws_sk, wave, lane, wm, wn, r, g);
     k_step<BN, STAGES, 1>(acc, src, kb + 1, KB, as_sk, ws_sk, wave, lane, wm, wn, r, g);
-    if constexpr (STAGES == 3) k_step<BN, STAGES, 2>(acc, src, kb + 2, KB, as_sk, ws_sk, wave, lane, wm, wn, r, g);
+    if constexpr (STAGES >= 3) k_step<BN, STAGES, 2>(acc, src, kb + 2, KB, as_sk, ws_sk, wave, lane, wm, wn, r, g);
+    if constexpr (STAGES >= 4) k_step<BN, STAGES, 3>(acc, src, kb + 3, KB, as_sk, ws_sk, wave, lane, wm, wn, r, g);
   }
   wait_vm_lgkm0<0>();  // no DMA may still target LDS when the workgroup ends
 
@@ -282,20 +293,24 @@ int launch_tile_dma(const uint8_t* q, int64_t ldq, const float* as, int64_t as_s
   const int vec_out = (ldo % 4) == 0 && (reinterpret_cast<uintptr_t>(out) % 8) == 0;
   dim3 grid(static_cast<unsigned>(tiles_m * tiles_n));
   uint16_t* o = static_cast<uint16_t*>(out);
-  // Two stages (76 KiB, room for the 160-wide W tile) let two workgroups share a CU,
-  // which measured faster than three stages and one workgroup per CU.
-  constexpr int stages = 2;
+  // Two stages (76 KiB, room for the 160-wide W tile) let two workgroups share a CU.
+  // When the tiles do not fill the CUs anyway, each K step waits on its DMA round trip,
+  // so a deeper ring (one workgroup per CU) keeps more K groups in flight.
+  const int stages = tiles_m * tiles_n <= device_cus() ? MI355X_DMA_STAGES_FEW : MI355X_DMA_STAGES_MANY;
 #define MI355X_DMA_ARGS q, ldq, as, as_sk, w, ldw, ws, ws_sn, ws_sk, o, ldo, M, N, K / kGroup, tiles_m, tiles_n, vec_out
-  if (bn == 160) {
-    if (out_dtype == kBF16) tile_gemm_dma_kernel<stages, 160, bf16_t><<<grid, kDmaThreads, 0, stream>>>(MI355X_DMA_ARGS);
-    else tile_gemm_dma_kernel<stages, 160, f16_t><<<grid, kDmaThreads, 0, stream>>>(MI355X_DMA_ARGS);
-  } else if (bn == 64) {
-    if (out_dtype == kBF16) tile_gemm_dma_kernel<stages, 64, bf16_t><<<grid, kDmaThreads, 0, stream>>>(MI355X_DMA_ARGS);
-    else tile_gemm_dma_kernel<stages, 64, f16_t><<<grid, kDmaThreads, 0, stream>>>(MI355X_DMA_ARGS);
-  } else {
-    if (out_dtype == kBF16) tile_gemm_dma_kernel<stages, 128, bf16_t><<<grid, kDmaThreads, 0, stream>>>(MI355X_DMA_ARGS);
-    else tile_gemm_dma_kernel<stages, 128, f16_t><<<grid, kDmaThreads, 0, stream>>>(MI355X_DMA_ARGS);
-  }
+#define MI355X_DMA_LAUNCH(ST, BN)                                                                                  \
+  (out_dtype == kBF16 ? tile_gemm_dma_kernel<ST, BN, bf16_t><<<grid, kDmaThreads, 0, stream>>>(MI355X_DMA_ARGS) \
+                      : tile_gemm_dma_kernel<ST, BN, f16_t><<<grid, kDmaThreads, 0, stream>>>(MI355X_DMA_ARGS))
+#define MI355X_DMA_BY_BN(ST)                \
+  do {                                      \
+    if (bn == 160) MI355X_DMA_LAUNCH(ST, 160); \
+    else if (bn == 64) MI355X_DMA_LAUNCH(ST, 64); \
+    else MI355X_DMA_LAUNCH(ST, 128);        \
+  } while (0)
+  if (stages == MI355X_DMA_STAGES_MANY) MI355X_DMA_BY_BN(MI355X_DMA_STAGES_MANY);
+  else MI355X_DMA_BY_BN(MI355X_DMA_STAGES_FEW);
+#undef MI355X_DMA_BY_BN
+#undef MI355X_DMA_LAUNCH
 #undef MI355X_DMA_ARGS
   return hipGetLastError() == hipSuccess ? MI355X_FP8_OK : MI355X_FP8_ERR_LAUNCH;
 }
