@@ -294,6 +294,14 @@ def test_prefill_2048_full_size(gpu, shape):
     (2048, 6144, 256),    # qkv width: 256x192 tiles
     (2048, 19456, 128),   # gate_up width: 256x224 tiles, last tile partial
     (2048, 8192, 128),    # 256x256 tiles
+    # Ring depth: three stages when the tiles fit within the CUs, two otherwise; K of 1 to
+    # 5 groups exercises the prologue and the unrolled loop's tail at both depths.
+    (300, 200, 128),      # 3 stages, one K group
+    (65, 128, 256),       # 3 stages, a single tile
+    (129, 640, 384),      # 3 stages, three K groups
+    (200, 2560, 512),     # 3 stages, four K groups
+    (536, 2560, 640),     # 3 stages, five K groups
+    (4096, 2560, 384),    # 2 stages (512 tiles), odd K-group count
 ], ids=lambda v: str(v))
 def test_prefill_tile_widths(gpu, rows, n, k):
     """Every tile width the prefill dispatch picks, against the oracle (the widths follow
