@@ -313,34 +313,74 @@ int64_t device_cus() {
   return cached[dev];
 }
 
-// Prefill kernel choice when the LDS-DMA kernels can run: the 256-row kernel at its best
-// tile width (256, 224 or 192), or the 128-row kernel (two workgroups per CU) at width 128,
-// 160 or 64, whichever has the smallest cost = the largest per-CU share of padded tile area,
-// ceil(tiles / CUs) x rows x width, with the 128-row kernel's weighted by 1.2 for its
-// lower MFMA rate per CU.  On the Qwen3-4B shapes at M = 2048 this picks 256x192 for qkv
-// (256 tiles), 256x224 for gate_up (696), 128x160 for o_proj and down (256).
+// Prefill kernel choice when the LDS-DMA kernels can run, from measured wave times.  Each
+// K step waits for its operands (a fifth of the lines miss L2), so a wave of tiles costs
+// about the same whatever the tile width, and the deeper rings of the narrower tiles make
+// their steps shorter.  Time of one full wave of tiles over K = 2560 on MI355X (µs, every
+// CU busy; the DMA kernel's second figure is for two workgroups per CU, the layout it
+// takes when the tiles outnumber the CUs):
+//   256 x 256 / 224 / 192 (two stages)   52.7  48.8  42.7
+//   256 x 160 / 128 (three stages)       38.1  31.8
+//   128 x 160 / 128 / 64 (three stages)  25.5  21.3  14.3   (two per CU: 45.3  31.1  21.7)
+// A last, partly filled wave costs 0.7 + 0.3 x its fill of a full one (a half-filled wave
+// measured 0.79-0.95).  Every kernel gives the same bits, so the choice may follow M.
 #ifndef MI355X_PREFILL_POLICY
 #define MI355X_PREFILL_POLICY 0  // 0: cost model, 1: always 256-row, 2: always 128-row
 #endif
+namespace {
+struct TileVariant {
+  int rows, bn;
+  double wave_one;  // µs per full wave, one workgroup per CU
+  double wave_two;  // µs per full wave of two workgroups per CU (0: not used)
+};
+constexpr TileVariant kTileVariants[] = {
+    {256, 256, 52.7, 0.0}, {256, 224, 48.8, 0.0}, {256, 192, 42.7, 0.0}, {256, 160, 38.1, 0.0},
+    {256, 128, 31.8, 0.0}, {128, 160, 25.5, 45.3}, {128, 128, 21.3, 31.1}, {128, 64, 14.3, 21.7},
+};
+
+double waves_cost(int64_t tiles, int64_t slots, double wave) {
+  const int64_t full = tiles / slots, rem = tiles % slots;
+  return wave * (static_cast<double>(full) + (rem ? 0.7 + 0.3 * static_cast<double>(rem) / slots : 0.0));
+}
+
+double variant_cost(const TileVariant& v, int64_t M, int64_t N, int64_t cus) {
+  const int64_t tiles = cdiv(M, v.rows) * cdiv(N, v.bn);
+  if (v.wave_two == 0.0 || tiles <= cus) return waves_cost(tiles, cus, v.wave_one);
+  return waves_cost(tiles, 2 * cus, v.wave_two);
+}
+
 struct PrefillChoice {
   bool rows256;
   int bn;
 };
-static PrefillChoice choose_prefill(int64_t M, int64_t N, int64_t cus) {
-  const int bn256 = tile256_width(M, N, cus);
-  const int64_t cost256 = cdiv(cdiv(M, 256) * cdiv(N, bn256), cus) * 256 * bn256;
-  int bn128 = 128;
-  int64_t cost128 = 0;
-  for (int bn : {128, 160, 64}) {
-    const int64_t cost = cdiv(cdiv(M, 128) * cdiv(N, bn), cus) * 128 * bn * 6 / 5;
-    if (cost128 == 0 || cost < cost128) {
-      cost128 = cost;
-      bn128 = bn;
+
+PrefillChoice choose_prefill(int64_t M, int64_t N, int64_t cus) {
+  PrefillChoice best{true, 256};
+  double best_cost = -1.0;
+  for (const TileVariant& v : kTileVariants) {
+    if ((MI355X_PREFILL_POLICY == 1 && v.rows != 256) || (MI355X_PREFILL_POLICY == 2 && v.rows != 128)) continue;
+    const double cost = variant_cost(v, M, N, cus);
+    if (best_cost < 0.0 || cost < best_cost) {
+      best = {v.rows == 256, v.bn};
+      best_cost = cost;
     }
   }
-  if (MI355X_PREFILL_POLICY == 1) return {true, bn256};
-  if (MI355X_PREFILL_POLICY == 2) return {false, bn128};
-  return cost256 <= cost128 ? PrefillChoice{true, bn256} : PrefillChoice{false, bn128};
+  return best;
+}
+}  // namespace
+
+int tile256_width(int64_t M, int64_t N, int64_t cus) {
+  int best = 256;
+  double best_cost = -1.0;
+  for (const TileVariant& v : kTileVariants) {
+    if (v.rows != 256) continue;
+    const double cost = variant_cost(v, M, N, cus);
+    if (best_cost < 0.0 || cost < best_cost) {
+      best = v.bn;
+      best_cost = cost;
+    }
+  }
+  return best;
 }
 
 template <int NT, int AF, bool ALIGNED, typename OutT>

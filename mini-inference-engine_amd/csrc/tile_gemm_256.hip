@@ -11,9 +11,11 @@
 // 2 * BM * BN * 128 flops; at 256x256 that is 22 B/clk at 70 % of the fp8 MFMA peak,
 // where 128x128 would need 44 B/clk, more than L2 delivers.
 //
-// Tile width BN (256, 224 or 192): chosen per launch so that the tile count fills the
-// CUs (the Qwen3-4B qkv projection at M = 2048 has 192 tiles of 256x256 but exactly 256
-// of 256x192; gate_up has 608 tiles of 256x256, 2.4 waves, but 696 of 256x224, 2.7 waves).
+// Tile width BN: 256, 224 or 192 with a two-stage LDS ring, or 160 or 128 with a
+// three-stage ring (3 x 52 KiB), which keeps two K groups in flight: the steps wait on their
+// operands' L2 misses, so the narrower tiles with the deeper ring finish a wave sooner.
+// The width is chosen per launch from measured wave times (the Qwen3-4B qkv projection at
+// M = 2048 gets exactly 256 tiles of 256x192; at M = 1024, 192 tiles of 256x128).
 //
 // Layout: 512 threads = 8 waves (2 per SIMD), wave w owns output rows 64 (w & 3) .. +63
 // and columns BN/2 (w >> 2) .. +BN/2-1, i.e. 4 x BN/32 MFMA tiles.
@@ -45,6 +47,12 @@ constexpr int kStageU4 = 2 * kXTileChunks;  // room for the widest W tile (256 r
 
 __shared__ uint4 t256_stage0[kStageU4];
 __shared__ uint4 t256_stage1[kStageU4];
+// Three-stage ring for tiles up to 160 wide: 3 x (160 + 256) x 128 B = 156 KiB.
+constexpr int kMaxBN3 = 160;
+constexpr int kStage3U4 = (kMaxBN3 + kRowsT) * 8;
+__shared__ uint4 t256_ring0[kStage3U4];
+__shared__ uint4 t256_ring1[kStage3U4];
+__shared__ uint4 t256_ring2[kStage3U4];
 
 typedef __attribute__((address_space(3))) void lds_void_t;
 
@@ -67,10 +75,16 @@ __device__ __forceinline__ void dma16(const uint8_t* base, uint32_t off, void* l
                : "memory");
 }
 
-template <int S>
+template <int NS, int S>
 __device__ __forceinline__ uint4* stage256() {
-  if constexpr (S == 0) return t256_stage0;
-  else return t256_stage1;
+  if constexpr (NS == 2) {
+    if constexpr (S == 0) return t256_stage0;
+    else return t256_stage1;
+  } else {
+    if constexpr (S == 0) return t256_ring0;
+    else if constexpr (S == 1) return t256_ring1;
+    else return t256_ring2;
+  }
 }
 
 // Tile geometry for width BN.
@@ -97,10 +111,10 @@ struct Src256 {
 
 // Fills stage S with K group kb.  W blocks past the tile (BN/8 not a multiple of 8) repeat
 // the last block: the two waves write identical bytes.
-template <int BN, int S>
+template <int BN, int NS, int S>
 __device__ __forceinline__ void issue256(const Src256& src, const uint8_t* w, const uint8_t* q, int64_t kb, int wave) {
   using G = Geo<BN>;
-  uint4* st = stage256<S>();
+  uint4* st = stage256<NS, S>();
   const uint8_t* wk = w + kb * kGroup;
   const uint8_t* qk = q + kb * kGroup;
 #pragma unroll
@@ -114,11 +128,11 @@ __device__ __forceinline__ void issue256(const Src256& src, const uint8_t* w, co
 
 // One of the step's DMA instructions: t < kWPerWave loads W block 8 t + wave, the rest the
 // activation blocks.
-template <int BN, int S>
+template <int BN, int NS, int S>
 __device__ __forceinline__ void issue_one(const Src256& src, const uint8_t* w, const uint8_t* q, int64_t kb, int wave,
                                           int t) {
   using G = Geo<BN>;
-  uint4* st = stage256<S>();
+  uint4* st = stage256<NS, S>();
   if (t < G::kWPerWave) {
     const int blk = (t * 8 + wave) < G::kWBlocks ? (t * 8 + wave) : (G::kWBlocks - 1);
     dma16(w + kb * kGroup, src.w[t], st + blk * 64);
@@ -148,14 +162,14 @@ struct Scales {
 // next K group (into the other stage, kn) go out in two halves, before the first and
 // before the middle MFMA group: a wave then never sits behind its whole DMA batch while
 // its partner wave on the SIMD does the same (measured 2-5 % faster than one batch).
-template <int BN, int S>
+template <int BN, int NS, int S, int NXT>
 __device__ __forceinline__ void compute256(v4f (&acc)[Geo<BN>::kNI][4], const Scales& sc_in, uint32_t use_b, int wm,
                                            int wn, int r, int g, const Src256& src, const uint8_t* w,
                                            const uint8_t* q, int64_t kn, int wave) {
   using G = Geo<BN>;
   constexpr int NI = G::kNI;
   constexpr int NDMA = G::kWPerWave + 4;
-  const uint4* st = stage256<S>();
+  const uint4* st = stage256<NS, S>();
   const int wrow0 = wn * (BN / 2) + r;
   v8i a0 = frag<S>(st, wrow0, g);
   v8i b[4];
@@ -166,7 +180,7 @@ __device__ __forceinline__ void compute256(v4f (&acc)[Geo<BN>::kNI][4], const Sc
   for (int i = 0; i < NI; ++i) {
 #pragma unroll
     for (int t = 0; t < NDMA; ++t)
-      if ((t < NDMA / 2 ? 0 : NI / 2) == i) issue_one<BN, S ^ 1>(src, w, q, kn, wave, t);
+      if ((t < NDMA / 2 ? 0 : NI / 2) == i) issue_one<BN, NS, NXT>(src, w, q, kn, wave, t);
     v8i a2;
     if (i + 2 < NI) a2 = frag<S>(st, wrow0 + 16 * (i + 2), g);
     const float wsv = (use_b >> i) & 1 ? sc_in.wb : sc_in.wa;
@@ -188,8 +202,10 @@ __device__ __forceinline__ void compute256(v4f (&acc)[Geo<BN>::kNI][4], const Sc
 // the workgroup barrier: after it every wave's DMA has landed and nobody reads the current
 // stage any more.  The wait sits at the end of a step, not the start, so that the loop's
 // back edge follows it directly (the compiler then needs no wait of its own before the reads).
+template <int N = 0>
 __device__ __forceinline__ void sync_stage() {
-  __builtin_amdgcn_s_waitcnt(0x70);  // vmcnt(0) lgkmcnt(0)
+  static_assert(N >= 0 && N < 64, "vmcnt immediate");
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4));  // vmcnt(N) lgkmcnt(0)
   __builtin_amdgcn_s_barrier();
 }
 
@@ -202,26 +218,30 @@ __device__ __forceinline__ void load_scales(Scales& s, const Src256& src, int64_
   s.wb = src.ws_b[kb * ws_sk + src.vzero];
 }
 
-// One K group kb of the range [.., khi).  The scales of K group kb + 1 go to registers
-// (per-lane loads, L2 hits), issued before the DMA loads so that the end-of-step wait also
-// covers them; the two unrolled steps alternate between two register sets.  Past the end
-// of the range the loads repeat its last group (the stage they fill is not read again).
-template <int BN, int CUR>
+// One K group kb of the range [.., khi), multiplied from ring stage CUR of NS.  The scales
+// of K group kb + 1 go to registers (per-lane loads, L2 hits), issued before the DMA loads
+// so that the end-of-step wait also covers them.  The DMA refills the stage NS - 1 groups
+// ahead (the one read in the previous step); the end-of-step wait leaves only that newest
+// batch in flight (loads complete in issue order).  Past the end of the range the loads
+// repeat its last group (the stage they fill is not read again).
+template <int BN, int NS, int CUR>
 __device__ __forceinline__ void step256(v4f (&acc)[Geo<BN>::kNI][4], const Scales& cur, Scales& next,
                                         const Src256& src, const uint8_t* w, const uint8_t* q, int64_t kb,
                                         int64_t khi, int64_t as_sk, int64_t ws_sk, int wave, int wm, int wn, int r,
                                         int g) {
+  constexpr int NDMA = Geo<BN>::kWPerWave + 4;
   const int64_t kn = kb + 1 < khi ? kb + 1 : khi - 1;
+  const int64_t kd = kb + NS - 1 < khi ? kb + NS - 1 : khi - 1;
   load_scales(next, src, kn, as_sk, ws_sk);
   // Keep the scale loads ahead of the DMA loads (compiler and scheduler barriers).
   asm volatile("" ::: "memory");
   __builtin_amdgcn_sched_barrier(0);
-  compute256<BN, CUR>(acc, cur, src.use_b, wm, wn, r, g, src, w, q, kn, wave);
+  compute256<BN, NS, CUR, (CUR + NS - 1) % NS>(acc, cur, src.use_b, wm, wn, r, g, src, w, q, kd, wave);
   // Every MFMA of the step is issued before the wait: the matrix core then works through
   // them while the wave waits for its DMA and the other waves (without this barrier the
   // scheduler moves the last MFMA groups behind s_barrier; measured 7 % slower on qkv).
   __builtin_amdgcn_sched_barrier(0);
-  sync_stage();
+  sync_stage<NDMA * (NS - 2)>();
 }
 
 __device__ __forceinline__ void tile_order(int64_t pid, int64_t tiles_m, int64_t tiles_n, int64_t* tm, int64_t* tn) {
@@ -291,27 +311,52 @@ __device__ __forceinline__ void setup_tile(Src256& src, const Dims256& d, int64_
   src.use_b = use_b;
 }
 
-// acc = the tile's products over K groups [klo, khi), in increasing order.
-template <int BN>
+// acc = the tile's products over K groups [klo, khi), in increasing order, through a ring
+// of NS (2 or 3) LDS stages.
+template <int BN, int NS>
 __device__ __forceinline__ void run_k(v4f (&acc)[Geo<BN>::kNI][4], const Src256& src, const Dims256& d, int64_t klo,
                                       int64_t khi, int wave, int wm, int wn, int r, int g) {
+  static_assert(NS == 2 || (NS == 3 && BN <= kMaxBN3), "ring depth");
+  constexpr int NDMA = Geo<BN>::kWPerWave + 4;
 #pragma unroll
   for (int i = 0; i < Geo<BN>::kNI; ++i)
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
-  Scales s_even, s_odd;
-  load_scales(s_even, src, klo, d.as_sk, d.ws_sk);
-  asm volatile("" ::: "memory");
-  __builtin_amdgcn_sched_barrier(0);
-  issue256<BN, 0>(src, d.w, d.q, klo, wave);
-  __builtin_amdgcn_sched_barrier(0);
-  sync_stage();
-  int64_t kb = klo;
-  for (; kb + 1 < khi; kb += 2) {
-    step256<BN, 0>(acc, s_even, s_odd, src, d.w, d.q, kb, khi, d.as_sk, d.ws_sk, wave, wm, wn, r, g);
-    step256<BN, 1>(acc, s_odd, s_even, src, d.w, d.q, kb + 1, khi, d.as_sk, d.ws_sk, wave, wm, wn, r, g);
+#define MI355X_STEP(CUR, SC, SN, KB) \
+  step256<BN, NS, CUR>(acc, SC, SN, src, d.w, d.q, KB, khi, d.as_sk, d.ws_sk, wave, wm, wn, r, g)
+  if constexpr (NS == 2) {
+    Scales s_even, s_odd;
+    load_scales(s_even, src, klo, d.as_sk, d.ws_sk);
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+    issue256<BN, 2, 0>(src, d.w, d.q, klo, wave);
+    __builtin_amdgcn_sched_barrier(0);
+    sync_stage();
+    int64_t kb = klo;
+    for (; kb + 1 < khi; kb += 2) {
+      MI355X_STEP(0, s_even, s_odd, kb);
+      MI355X_STEP(1, s_odd, s_even, kb + 1);
+    }
+    if (kb < khi) MI355X_STEP(0, s_even, s_odd, kb);
+  } else {
+    Scales s0, s1, s2;
+    load_scales(s0, src, klo, d.as_sk, d.ws_sk);
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+    issue256<BN, 3, 0>(src, d.w, d.q, klo, wave);
+    issue256<BN, 3, 1>(src, d.w, d.q, klo + 1 < khi ? klo + 1 : khi - 1, wave);
+    __builtin_amdgcn_sched_barrier(0);
+    sync_stage<NDMA>();  // stage 0 and the scales landed; stage 1 may still be in flight
+    int64_t kb = klo;
+    for (; kb + 2 < khi; kb += 3) {
+      MI355X_STEP(0, s0, s1, kb);
+      MI355X_STEP(1, s1, s2, kb + 1);
+      MI355X_STEP(2, s2, s0, kb + 2);
+    }
+    if (kb < khi) MI355X_STEP(0, s0, s1, kb);
+    if (kb + 1 < khi) MI355X_STEP(1, s1, s2, kb + 1);
   }
-  if (kb < khi) step256<BN, 0>(acc, s_even, s_odd, src, d.w, d.q, kb, khi, d.as_sk, d.ws_sk, wave, wm, wn, r, g);
+#undef MI355X_STEP
 }
 
 // Lane holds out[m = m0 + 64 wm + 16 j + r][n = n0 + BN/2 wn + 16 i + 4 g + v].
@@ -342,7 +387,7 @@ __device__ __forceinline__ void store_tile(const v4f (&acc)[Geo<BN>::kNI][4], co
   }
 }
 
-template <int BN, typename OutT>
+template <int BN, int NS, typename OutT>
 __global__ __launch_bounds__(kT256Threads, 2) void tile256_gemm_kernel(Dims256 d, int64_t tiles_m, int64_t tiles_n) {
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -357,42 +402,25 @@ __global__ __launch_bounds__(kT256Threads, 2) void tile256_gemm_kernel(Dims256 d
   asm volatile("v_mov_b32 %0, 0" : "=v"(src.vzero));
   setup_tile<BN>(src, d, tm * kRowsT, tn * BN, wave, lane, wm, wn, r);
   v4f acc[Geo<BN>::kNI][4];
-  run_k<BN>(acc, src, d, 0, d.KB, wave, wm, wn, r, g);
+  run_k<BN, NS>(acc, src, d, 0, d.KB, wave, wm, wn, r, g);
   __builtin_amdgcn_s_waitcnt(0x70);  // no DMA may still target LDS when the workgroup ends
   store_tile<BN, OutT>(acc, d, tm * kRowsT, tn * BN, wm, wn, r, g);
 }
 
-template <int BN>
+template <int BN, int NS>
 int launch_bn(const Dims256& d, int out_dtype, hipStream_t stream) {
   const int64_t tiles_m = (d.M + kRowsT - 1) / kRowsT;
   const int64_t tiles_n = (d.N + BN - 1) / BN;
   if (tiles_m * tiles_n > 0x7fffffffLL) return MI355X_FP8_ERR_UNSUPPORTED;
   const dim3 grid(static_cast<unsigned>(tiles_m * tiles_n));
   if (out_dtype == kBF16)
-    tile256_gemm_kernel<BN, bf16_t><<<grid, kT256Threads, 0, stream>>>(d, tiles_m, tiles_n);
+    tile256_gemm_kernel<BN, NS, bf16_t><<<grid, kT256Threads, 0, stream>>>(d, tiles_m, tiles_n);
   else
-    tile256_gemm_kernel<BN, f16_t><<<grid, kT256Threads, 0, stream>>>(d, tiles_m, tiles_n);
+    tile256_gemm_kernel<BN, NS, f16_t><<<grid, kT256Threads, 0, stream>>>(d, tiles_m, tiles_n);
   return hipGetLastError() == hipSuccess ? MI355X_FP8_OK : MI355X_FP8_ERR_LAUNCH;
 }
 
 }  // namespace
-
-int tile256_width(int64_t M, int64_t N, int64_t cus) {
-  // Fewest workgroup waves over the CUs, then the least padded area, then the widest tile.
-  const int64_t tiles_m = (M + kRowsT - 1) / kRowsT;
-  int best = 256;
-  double best_cost = 0.0;
-  for (int bn : {256, 224, 192}) {
-    const int64_t tiles = tiles_m * ((N + bn - 1) / bn);
-    const int64_t waves = (tiles + cus - 1) / cus;
-    const double cost = static_cast<double>(waves) * bn;  // time ~ waves x per-tile work
-    if (best_cost == 0.0 || cost < best_cost) {
-      best = bn;
-      best_cost = cost;
-    }
-  }
-  return best;
-}
 
 int launch_tile256(const uint8_t* q, int64_t ldq, const float* as, int64_t as_sk, const uint8_t* w,
                    int64_t ldw, const float* ws, int64_t ws_sn, int64_t ws_sk, void* out, int out_dtype,
@@ -403,9 +431,11 @@ int launch_tile256(const uint8_t* q, int64_t ldq, const float* as, int64_t as_sk
   const Dims256 d{q, as, w, ws, static_cast<uint16_t*>(out), ldq, as_sk, ldw, ws_sn, ws_sk, ldo, M, N, K / kGroup,
                   (ldo % 4) == 0 && (reinterpret_cast<uintptr_t>(out) % 8) == 0};
   switch (bn) {
-    case 256: return launch_bn<256>(d, out_dtype, stream);
-    case 224: return launch_bn<224>(d, out_dtype, stream);
-    case 192: return launch_bn<192>(d, out_dtype, stream);
+    case 256: return launch_bn<256, 2>(d, out_dtype, stream);
+    case 224: return launch_bn<224, 2>(d, out_dtype, stream);
+    case 192: return launch_bn<192, 2>(d, out_dtype, stream);
+    case 160: return launch_bn<160, 3>(d, out_dtype, stream);  // three-stage ring
+    case 128: return launch_bn<128, 3>(d, out_dtype, stream);
     default: return MI355X_FP8_ERR_INVALID;
   }
 }
