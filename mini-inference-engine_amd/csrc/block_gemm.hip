@@ -14,12 +14,13 @@
 // A and B, so the dot product is unchanged, and every load instruction reads whole 64-byte
 // row halves.
 //
-// Two kernels:
+// Kernels here:
 //   stream_gemm_kernel  decode-sized M (<= 64 rows per launch slice).  HBM-bound weight
-//                       streaming: each workgroup owns 16 or 32 W rows over the whole of
-//                       K, W goes global -> registers (every byte read once, D K groups in
-//                       flight per wave), the small activation matrix is served from L2,
-//                       and the sixteen waves' K-partials combine in LDS.  No workspace, no
+//   (+ rounds variant)  streaming: each workgroup owns 16 or 32 W rows over the whole of
+//                       K, W goes global -> registers (every byte read once, one K group in
+//                       flight per wave), the small activation matrix is served from L2;
+//                       the K groups' MFMA partials meet in LDS and are folded in K order,
+//                       so the bits equal the prefill kernels'.  No workspace, no
 //                       cross-workgroup synchronisation.
 //   tile_gemm_kernel    prefill-sized M.  MFMA-bound: 128x128 output tile per 256-thread
 //                       workgroup, 2x2 waves of 64x64, K groups staged global -> registers
@@ -36,30 +37,41 @@ constexpr int kThreads = 256;  // tile kernel
 // Stream kernel (decode M)
 // ------------------------------------------------------------------------------------
 // One workgroup owns 16*AF consecutive W rows and reads them over the whole of K exactly
-// once.  Its WAVES waves take K groups round-robin (wave w: w, w + WAVES, ...), each
-// keeping D groups of loads in flight, and combine their fp32 partials through LDS in
-// wave order.  16 waves with one group in flight each measured best on the Qwen3-4B
-// shapes (8 or 4 waves with 2-4 groups in flight were 5-20 % slower).  The assignment of K groups to waves depends on K alone, so a row's result
-// is the same whatever M is or whichever projections are concatenated along N.
-#ifndef MI355X_STREAM_WAVES
-#define MI355X_STREAM_WAVES 16
-#endif
-#ifndef MI355X_STREAM_DEPTH
-#define MI355X_STREAM_DEPTH 1
-#endif
-constexpr int kStreamWaves = MI355X_STREAM_WAVES;
-constexpr int kStreamDepth = MI355X_STREAM_DEPTH;
+// once.  Its 16 waves take K groups round-robin (wave w: w, w + 16, ...) with the next
+// group's loads in flight, and compute each group's MFMA partial; the partials then meet
+// in LDS, where one thread per output element folds them in K order (below).  16 waves
+// with one group in flight each measured best on the Qwen3-4B shapes.
+constexpr int kStreamWaves = 16;
+// One-round partial buffer limit: two workgroups of 1024 threads share a CU's 160 KiB.
+constexpr size_t kStreamFoldLds = 80 * 1024;
 
+__host__ __device__ constexpr size_t stream_fold_bytes(int64_t kb, int af, int nt) {
+  return static_cast<size_t>(kb) * (static_cast<size_t>(af) * nt * 256 + 16 * nt) * sizeof(float);
+}
+
+// The fold: the waves publish each K group's raw MFMA partials and the scale products
+// a_s * w_s in LDS, and one thread per output element folds acc = fma(partial, a_s * w_s,
+// acc) over the K groups in increasing order -- the fold of every prefill kernel, on
+// bit-identical MFMA partials (same operands, same K order within the instruction).  A
+// row's bits are then the same for every M and every kernel, so the dispatch may pick any
+// kernel for any shape.
+//
+// stream_rounds_kernel: for when the partials of all K groups do not fit in LDS at once.
+// It works in rounds of kStreamWaves consecutive groups (one per wave), each published,
+// folded and followed by the next; the next round's loads are issued before the publish
+// and fold, so they overlap them.
 template <int NT, int AF, bool ALIGNED, typename OutT>
-__global__ __launch_bounds__(kStreamWaves * 64) void stream_gemm_kernel(
+__global__ __launch_bounds__(kStreamWaves * 64) void stream_rounds_kernel(
     const uint8_t* __restrict__ q, int64_t ldq, const float* __restrict__ as, int64_t as_sm,
     int64_t as_sk, const uint8_t* __restrict__ w, int64_t ldw, const float* __restrict__ ws,
     int64_t ws_sn, int64_t ws_sk, uint16_t* __restrict__ out, int64_t ldo, int64_t M, int64_t N,
     int64_t K, int64_t KB) {
-  constexpr int kRows = 16 * AF;            // W rows of this workgroup
-  constexpr int kTok = 16 * NT;             // token rows of this slice
-  constexpr int kStride = kRows + 4;        // padded LDS row (floats)
-  __shared__ float red[kStreamWaves * kTok * kStride];
+  constexpr int kRows = 16 * AF;  // W rows of this workgroup
+  constexpr int kTok = 16 * NT;   // token rows of this slice
+  constexpr int kBufs = AF * NT >= 4 ? 1 : 2;  // double-buffered publish when it fits
+  constexpr int kTiles = AF * NT;
+  __shared__ float4 part[kBufs][kStreamWaves][kTiles][64];  // raw partials, lane layout
+  __shared__ float scl[kBufs][kStreamWaves][kTok];          // a_s * w_s per token
 
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
@@ -70,76 +82,184 @@ __global__ __launch_bounds__(kStreamWaves * 64) void stream_gemm_kernel(
   const int64_t m_base = static_cast<int64_t>(blockIdx.z) * 64;
   const int64_t m_rows = (M - m_base) < kTok ? (M - m_base) : kTok;
   const int64_t nb = n0 / kGroup;
-
-  v4f acc[AF][NT];
-#pragma unroll
-  for (int i = 0; i < AF; ++i)
-#pragma unroll
-    for (int j = 0; j < NT; ++j) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
-
-  // The wave index is uniform across the wave: make that visible to the compiler so that
-  // the K-group bookkeeping and the weight-scale loads stay scalar.
   const int64_t wave_u = __builtin_amdgcn_readfirstlane(wave);
-  for (int64_t kb0 = wave_u; kb0 < KB; kb0 += kStreamWaves * kStreamDepth) {
-    v8i a[kStreamDepth][AF];
-    v8i b[kStreamDepth][NT];
-    float asv[kStreamDepth][NT];
-    float wsv[kStreamDepth];
+
+  // This thread's output element in the fold (threads past the tile's elements only help
+  // compute partials).
+  const int e = tid;
+  const bool folder = e < kRows * kTok;
+  const int ftok = e / kRows, fnl = e - (e / kRows) * kRows;
+  const int fi = fnl >> 4, fj = ftok >> 4;
+  const int flane = (ftok & 15) + 16 * ((fnl & 15) >> 2), fv = fnl & 3;
+  float acc = 0.0f;
+
+  v8i a[AF], b[NT];
+  float asv[NT], wsv;
+  auto load = [&](int64_t kb) {  // kb < KB (callers skip groups past the end)
+    const int64_t kbc = kb;
+    const int64_t k_lo = kbc * kGroup + 16 * g;
 #pragma unroll
-    for (int d = 0; d < kStreamDepth; ++d) {
-      const int64_t kb = kb0 + d * kStreamWaves;
-      const int64_t kbc = kb < KB ? kb : KB - 1;  // clamped: loads stay in bounds, result unused
-      const int64_t k_lo = kbc * kGroup + 16 * g;
-#pragma unroll
-      for (int i = 0; i < AF; ++i) {
-        const int64_t row = n0 + 16 * i + r;
-        a[d][i] = pack_v8i(load_chunk16<ALIGNED>(w, ldw, row, N, k_lo, K),
-                           load_chunk16<ALIGNED>(w, ldw, row, N, k_lo + 64, K));
-      }
-      wsv[d] = ws[nb * ws_sn + kbc * ws_sk];
-#pragma unroll
-      for (int j = 0; j < NT; ++j) {
-        const int64_t tok = 16 * j + r;
-        const int64_t m = m_base + tok;
-        b[d][j] = pack_v8i(load_chunk16<ALIGNED>(q, ldq, m, M, k_lo, K),
-                           load_chunk16<ALIGNED>(q, ldq, m, M, k_lo + 64, K));
-        asv[d][j] = tok < m_rows ? as[m * as_sm + kbc * as_sk] : 0.0f;
-      }
+    for (int i = 0; i < AF; ++i) {
+      const int64_t row = n0 + 16 * i + r;
+      a[i] = pack_v8i(load_chunk16<ALIGNED>(w, ldw, row, N, k_lo, K), load_chunk16<ALIGNED>(w, ldw, row, N, k_lo + 64, K));
     }
+    wsv = ws[nb * ws_sn + kbc * ws_sk];
 #pragma unroll
-    for (int d = 0; d < kStreamDepth; ++d) {
-      if (kb0 + d * kStreamWaves >= KB) break;
+    for (int j = 0; j < NT; ++j) {
+      const int64_t tok = 16 * j + r;
+      const int64_t m = m_base + tok;
+      b[j] = pack_v8i(load_chunk16<ALIGNED>(q, ldq, m, M, k_lo, K), load_chunk16<ALIGNED>(q, ldq, m, M, k_lo + 64, K));
+      asv[j] = tok < m_rows ? as[m * as_sm + kbc * as_sk] : 0.0f;
+    }
+  };
+
+  if (wave_u < KB) load(wave_u);
+  int buf = 0;
+  for (int64_t t0 = 0; t0 < KB; t0 += kStreamWaves) {
+    const bool have = t0 + wave_u < KB;  // wave-uniform
+    const bool next = t0 + kStreamWaves + wave_u < KB;
+    v4f p[AF][NT];
+    if (have) {
 #pragma unroll
       for (int i = 0; i < AF; ++i)
 #pragma unroll
-        for (int j = 0; j < NT; ++j) {
-          const v4f p = mfma_16x16x128_e4m3(a[d][i], b[d][j]);
-          const float sc = asv[d][j] * wsv[d];
+        for (int j = 0; j < NT; ++j) p[i][j] = mfma_16x16x128_e4m3(a[i], b[j]);
+    }
+    float sc[NT];
 #pragma unroll
-          for (int v = 0; v < 4; ++v) acc[i][j][v] = __builtin_fmaf(p[v], sc, acc[i][j][v]);
-        }
+    for (int j = 0; j < NT; ++j) sc[j] = asv[j] * wsv;
+    // The next round's group, in flight during the publish and fold (unaligned shapes,
+    // whose loads are assembled from bytes, load after the fold to stay within registers).
+    if constexpr (ALIGNED) {
+      if (next) load(t0 + kStreamWaves + wave_u);
+    }
+    if constexpr (kBufs == 1) __syncthreads();  // the previous fold has read the buffer
+    if (have) {
+#pragma unroll
+      for (int i = 0; i < AF; ++i)
+#pragma unroll
+        for (int j = 0; j < NT; ++j)
+          part[buf][wave][i * NT + j][lane] = make_float4(p[i][j][0], p[i][j][1], p[i][j][2], p[i][j][3]);
+      if (g == 0) {
+#pragma unroll
+        for (int j = 0; j < NT; ++j) scl[buf][wave][16 * j + r] = sc[j];
+      }
+    }
+    __syncthreads();
+    if (folder) {
+      const int64_t nk = KB - t0 < kStreamWaves ? KB - t0 : kStreamWaves;
+      for (int x = 0; x < nk; ++x) {
+        const float* pv = reinterpret_cast<const float*>(&part[buf][x][fi * NT + fj][flane]);
+        acc = __builtin_fmaf(pv[fv], scl[buf][x][ftok], acc);
+      }
+    }
+    if constexpr (!ALIGNED) {
+      if (next) load(t0 + kStreamWaves + wave_u);
+    }
+    if constexpr (kBufs == 2) buf ^= 1;
+  }
+  if (folder && ftok < m_rows && n0 + fnl < N) out[(m_base + ftok) * ldo + n0 + fnl] = OutCvt<OutT>::cvt(acc);
+}
+
+// stream_gemm_kernel: the same arithmetic in one round, when every K group's partials fit
+// in LDS at once (dynamic LDS): each wave walks its K groups (w, w + 16, ...) with the
+// next group's loads in flight, publishes every partial, and after a single barrier one
+// thread per output element folds the whole K chain in order.
+extern __shared__ float4 stream_fold_lds[];
+
+template <int NT, int AF, bool ALIGNED, typename OutT>
+__global__ __launch_bounds__(kStreamWaves * 64) void stream_gemm_kernel(
+    const uint8_t* __restrict__ q, int64_t ldq, const float* __restrict__ as, int64_t as_sm,
+    int64_t as_sk, const uint8_t* __restrict__ w, int64_t ldw, const float* __restrict__ ws,
+    int64_t ws_sn, int64_t ws_sk, uint16_t* __restrict__ out, int64_t ldo, int64_t M, int64_t N,
+    int64_t K, int64_t KB) {
+  constexpr int kRows = 16 * AF;
+  constexpr int kTok = 16 * NT;
+  constexpr int kTiles = AF * NT;
+  // [KB][kTok][kRows] partials, element-major (the fold's reads are consecutive), then
+  // [KB][kTok] scale products.
+  float* part = reinterpret_cast<float*>(stream_fold_lds);
+  float* scl = part + KB * kTok * kRows;
+
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6;
+  const int lane = tid & 63;
+  const int r = lane & 15;
+  const int g = lane >> 4;
+  const int64_t n0 = static_cast<int64_t>(blockIdx.x) * kRows;
+  const int64_t m_base = static_cast<int64_t>(blockIdx.z) * 64;
+  const int64_t m_rows = (M - m_base) < kTok ? (M - m_base) : kTok;
+  const int64_t nb = n0 / kGroup;
+  const int64_t wave_u = __builtin_amdgcn_readfirstlane(wave);
+
+  v8i a[AF], b[NT];
+  float asv[NT], wsv;
+  auto load = [&](int64_t kb) {
+    const int64_t k_lo = kb * kGroup + 16 * g;
+#pragma unroll
+    for (int i = 0; i < AF; ++i) {
+      const int64_t row = n0 + 16 * i + r;
+      a[i] = pack_v8i(load_chunk16<ALIGNED>(w, ldw, row, N, k_lo, K), load_chunk16<ALIGNED>(w, ldw, row, N, k_lo + 64, K));
+    }
+    wsv = ws[nb * ws_sn + kb * ws_sk];
+#pragma unroll
+    for (int j = 0; j < NT; ++j) {
+      const int64_t tok = 16 * j + r;
+      const int64_t m = m_base + tok;
+      b[j] = pack_v8i(load_chunk16<ALIGNED>(q, ldq, m, M, k_lo, K), load_chunk16<ALIGNED>(q, ldq, m, M, k_lo + 64, K));
+      asv[j] = tok < m_rows ? as[m * as_sm + kb * as_sk] : 0.0f;
+    }
+  };
+  if (wave_u < KB) load(wave_u);
+  for (int64_t kb = wave_u; kb < KB; kb += kStreamWaves) {
+    v4f p[AF][NT];
+#pragma unroll
+    for (int i = 0; i < AF; ++i)
+#pragma unroll
+      for (int j = 0; j < NT; ++j) p[i][j] = mfma_16x16x128_e4m3(a[i], b[j]);
+    float sc[NT];
+#pragma unroll
+    for (int j = 0; j < NT; ++j) sc[j] = asv[j] * wsv;
+    if constexpr (ALIGNED) {
+      if (kb + kStreamWaves < KB) load(kb + kStreamWaves);  // in flight during the publish
+    }
+    // Lane holds D[n = 16 i + 4 g + v][tok = 16 j + r]: four consecutive n of one token.
+#pragma unroll
+    for (int i = 0; i < AF; ++i)
+#pragma unroll
+      for (int j = 0; j < NT; ++j)
+        *reinterpret_cast<float4*>(part + (kb * kTok + 16 * j + r) * kRows + 16 * i + 4 * g) =
+            make_float4(p[i][j][0], p[i][j][1], p[i][j][2], p[i][j][3]);
+    if (g == 0) {
+#pragma unroll
+      for (int j = 0; j < NT; ++j) scl[kb * kTok + 16 * j + r] = sc[j];
+    }
+    if constexpr (!ALIGNED) {
+      if (kb + kStreamWaves < KB) load(kb + kStreamWaves);
     }
   }
-
-  // Lane holds D[n = 16 i + 4 g + v][token = 16 j + r]; stage as red[wave][token][n].
-  float* mine = red + wave * kTok * kStride;
-#pragma unroll
-  for (int i = 0; i < AF; ++i)
-#pragma unroll
-    for (int j = 0; j < NT; ++j)
-      *reinterpret_cast<float4*>(mine + (16 * j + r) * kStride + 16 * i + 4 * g) =
-          make_float4(acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]);
   __syncthreads();
-  for (int e = tid; e < kTok * kRows; e += kStreamWaves * 64) {
-    const int tok = e / kRows;
-    const int nl = e - tok * kRows;
-    const int64_t n = n0 + nl;
-    if (tok >= m_rows || n >= N) continue;
-    float val = red[tok * kStride + nl];
+  const int e = tid;
+  if (e >= kRows * kTok) return;
+  const int tok = e / kRows, nl = e - (e / kRows) * kRows;
+  if (tok >= m_rows) return;  // padding token: nothing to fold
+  const float* pf = part + e;
+  const float* sf = scl + tok;
+  // Reads in batches of eight ahead of their FMAs, so the chain waits on LDS once per batch.
+  float acc = 0.0f;
+  int64_t kb = 0;
+  for (; kb + 8 <= KB; kb += 8) {
+    float pv[8], sv[8];
 #pragma unroll
-    for (int x = 1; x < kStreamWaves; ++x) val += red[x * kTok * kStride + tok * kStride + nl];
-    out[(m_base + tok) * ldo + n] = OutCvt<OutT>::cvt(val);
+    for (int x = 0; x < 8; ++x) {
+      pv[x] = pf[(kb + x) * kTok * kRows];
+      sv[x] = sf[(kb + x) * kTok];
+    }
+#pragma unroll
+    for (int x = 0; x < 8; ++x) acc = __builtin_fmaf(pv[x], sv[x], acc);
   }
+  for (; kb < KB; ++kb) acc = __builtin_fmaf(pf[kb * kTok * kRows], sf[kb * kTok], acc);
+  if (n0 + nl < N) out[(m_base + tok) * ldo + n0 + nl] = OutCvt<OutT>::cvt(acc);
 }
 
 // ------------------------------------------------------------------------------------
@@ -285,7 +405,16 @@ static int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 int plan_gemm(int64_t M, int64_t N, int64_t K, int config, GemmPlan* plan) {
   if (M < 0 || N < 0 || K <= 0) return MI355X_FP8_ERR_INVALID;
   *plan = GemmPlan{};
-  if (config == MI355X_FP8_CONFIG_AUTO) config = M <= 64 ? MI355X_FP8_CONFIG_STREAM : MI355X_FP8_CONFIG_TILE128;
+  if (config == MI355X_FP8_CONFIG_AUTO) {
+    // Every kernel gives the same bits, so this is a speed choice only.  The stream kernel
+    // re-reads the activations from L2 in every workgroup, so with more rows it keeps the
+    // lead only while the weight rows give few workgroups (measured on the Qwen3-4B
+    // shapes: at 64 rows o_proj / down 15 / 30 us streamed against 18 / 38 us tiled, qkv /
+    // gate_up 20 / 50 us against 13 / 22 us; at 32 rows gate_up 24 against 22 us).
+    const bool stream = M <= 16 || (M <= 64 && cdiv(N, 16) <= device_cus()) ||
+                        (M <= 32 && cdiv(N, 16) <= 2 * device_cus());
+    config = stream ? MI355X_FP8_CONFIG_STREAM : MI355X_FP8_CONFIG_TILE128;
+  }
   if (config != MI355X_FP8_CONFIG_STREAM && config != MI355X_FP8_CONFIG_TILE128 &&
       config != MI355X_FP8_CONFIG_TILE256)
     return MI355X_FP8_ERR_INVALID;
@@ -295,7 +424,10 @@ int plan_gemm(int64_t M, int64_t N, int64_t K, int config, GemmPlan* plan) {
   plan->token_tiles = slice_rows <= 16 ? 1 : (slice_rows <= 32 ? 2 : 4);
   // Two 16-row MFMA tiles per workgroup when N is wide enough to keep every CU busy
   // anyway: halves the L2 re-reads of the activations.
-  plan->row_tiles = (plan->token_tiles <= 2 && N >= 16384) ? 2 : 1;
+  plan->row_tiles = (plan->token_tiles <= 2 && N >= 16384 &&
+                     stream_fold_bytes(cdiv(K, kGroup), 2, plan->token_tiles) <= kStreamFoldLds)
+                        ? 2
+                        : 1;
   return MI355X_FP8_OK;
 }
 
@@ -388,8 +520,14 @@ static void launch_stream_t(const uint8_t* q, int64_t ldq, const float* as, int6
                             const uint8_t* w, int64_t ldw, const float* ws, int64_t ws_sn, int64_t ws_sk,
                             uint16_t* out, int64_t ldo, int64_t M, int64_t N, int64_t K, hipStream_t stream) {
   dim3 grid(static_cast<unsigned>(cdiv(N, 16 * AF)), 1, static_cast<unsigned>(cdiv(M, 64)));
-  stream_gemm_kernel<NT, AF, ALIGNED, OutT><<<grid, kStreamWaves * 64, 0, stream>>>(
-      q, ldq, as, as_sm, as_sk, w, ldw, ws, ws_sn, ws_sk, out, ldo, M, N, K, cdiv(K, kGroup));
+  const int64_t kb = cdiv(K, kGroup);
+  const size_t one_round = stream_fold_bytes(kb, AF, NT);
+  if (one_round <= kStreamFoldLds)
+    stream_gemm_kernel<NT, AF, ALIGNED, OutT><<<grid, kStreamWaves * 64, one_round, stream>>>(
+        q, ldq, as, as_sm, as_sk, w, ldw, ws, ws_sn, ws_sk, out, ldo, M, N, K, kb);
+  else
+    stream_rounds_kernel<NT, AF, ALIGNED, OutT><<<grid, kStreamWaves * 64, 0, stream>>>(
+        q, ldq, as, as_sm, as_sk, w, ldw, ws, ws_sn, ws_sk, out, ldo, M, N, K, kb);
 }
 
 template <bool ALIGNED, typename OutT>

@@ -348,3 +348,36 @@ def test_decode_linear_equals_quantizer_then_gemm(gpu, shape, rows, dtype):
     padded[:, : shape.k] = x
     got2 = fp8.mi355x_fp8_linear(padded.to(gpu)[:, : shape.k], wg, wsg, BLOCK)
     assert bitwise_equal(got2, ref), bit_mismatch_details(got2, ref)
+
+
+@pytest.mark.parametrize("shape", [ModelShape("tail", 193, 259), ModelShape("kv", 1024, 2560),
+                                   ModelShape("o", 2560, 4096)], ids=lambda s: s.name)
+@pytest.mark.parametrize("rows", [1, 7, 33, 129, 1000])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_reference_gate_every_config_bitwise_and_row_independent(gpu, shape, rows, dtype):
+    """The reference's exactness gate (tests/test_sm89_fp8_exact.py:14-38): every path and
+    every GEMM config give the same bits, and a row computed alone equals the same row in
+    the batch, for decode-sized and prefill-sized M alike.  Here every kernel folds the same
+    MFMA partials in the same K order, so this holds across the decode kernel and the
+    prefill kernels too.  (The 256-row config rejects K % 128 != 0: skipped for that shape.)"""
+
+    _note("gate", shape.name, rows, dtype)
+    x = make_activations(rows, shape.k, 42, dtype).to(gpu)
+    w, ws = make_weights(shape, 42)
+    wg, wsg = w.to(gpu), ws.to(gpu)
+    reference = fp8.mi355x_fp8_linear(x, wg, wsg, BLOCK, path="fused")
+    for path in ("auto", "split"):
+        actual = fp8.mi355x_fp8_linear(x, wg, wsg, BLOCK, path=path)
+        assert bitwise_equal(reference, actual), bit_mismatch_details(reference, actual)
+    selected = sorted(set(range(min(rows, 7))) | {rows - 1})
+    for row in selected:
+        single = fp8.mi355x_fp8_linear(x[row:row + 1], wg, wsg, BLOCK, path="fused")
+        assert bitwise_equal(single, reference[row:row + 1]), (row, bit_mismatch_details(single, reference[row:row + 1]))
+    for config in fp8.GEMM_CONFIGS:
+        if config.name == "tile256" and shape.k % 128:
+            continue
+        actual = fp8.mi355x_fp8_linear(x, wg, wsg, BLOCK, path="split", gemm_config=config)
+        assert bitwise_equal(reference, actual), f"{config.name}: {bit_mismatch_details(reference, actual)}"
+        for row in selected:
+            single = fp8.mi355x_fp8_linear(x[row:row + 1], wg, wsg, BLOCK, path="split", gemm_config=config)
+            assert bitwise_equal(single, actual[row:row + 1]), (config.name, row)
