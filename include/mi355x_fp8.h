@@ -30,7 +30,7 @@ extern "C" {
 
 /* GEMM kernel selection (the `gemm_config` of the reference's wrapper). */
 #define MI355X_FP8_CONFIG_AUTO 0
-#define MI355X_FP8_CONFIG_STREAM 1  /* weight-streaming split-K kernel, M <= 64 */
+#define MI355X_FP8_CONFIG_STREAM 1  /* weight-streaming decode kernel (auto: up to 64 rows) */
 #define MI355X_FP8_CONFIG_TILE128 2 /* LDS-tiled 128x128 MFMA kernel, any M */
 #define MI355X_FP8_CONFIG_TILE256 3 /* 256x256 MFMA kernel; needs K % 128 == 0, 16-byte
                                        aligned q/w and K-group-major activation scales */
