@@ -502,11 +502,13 @@ struct PrefillChoice {
   int bn;
 };
 
-PrefillChoice choose_prefill(int64_t M, int64_t N, int64_t cus) {
-  PrefillChoice best{true, 256};
+// rows256_ok: the 256-row kernel's 32-bit offsets reach every byte of q and W.
+PrefillChoice choose_prefill(int64_t M, int64_t N, int64_t cus, bool rows256_ok) {
+  PrefillChoice best{false, 128};
   double best_cost = -1.0;
   for (const TileVariant& v : kTileVariants) {
     if ((MI355X_PREFILL_POLICY == 1 && v.rows != 256) || (MI355X_PREFILL_POLICY == 2 && v.rows != 128)) continue;
+    if (v.rows == 256 && !rows256_ok) continue;
     const double cost = variant_cost(v, M, N, cus);
     if (best_cost < 0.0 || cost < best_cost) {
       best = {v.rows == 256, v.bn};
@@ -605,7 +607,7 @@ int launch_block_gemm(const GemmPlan& plan, const uint8_t* q, int64_t ldq, const
                           tile256_width(M, N, device_cus()), stream);
   }
   if (plan.kernel == MI355X_FP8_CONFIG_TILE128 && dma_ok) {
-    const PrefillChoice c = choose_prefill(M, N, device_cus());
+    const PrefillChoice c = choose_prefill(M, N, device_cus(), tile256_offsets_ok(ldq, ldw, M, N, K));
     if (c.rows256)
       return launch_tile256(q, ldq, as, as_sk, w, ldw, ws, ws_sn, ws_sk, out, out_dtype, ldo, M, N, K, c.bn, stream);
     return launch_tile_dma(q, ldq, as, as_sk, w, ldw, ws, ws_sn, ws_sk, out, out_dtype, ldo, M, N, K, c.bn, stream);

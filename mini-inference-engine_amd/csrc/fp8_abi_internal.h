@@ -56,6 +56,8 @@ int launch_tile256(const uint8_t* q, int64_t ldq, const float* as, int64_t as_sk
                    int64_t ldw, const float* ws, int64_t ws_sn, int64_t ws_sk, void* out, int out_dtype,
                    int64_t ldo, int64_t M, int64_t N, int64_t K, int bn, hipStream_t stream);
 int tile256_width(int64_t M, int64_t N, int64_t cus);
+// Whether the 256-row kernel's 32-bit byte offsets reach every byte of q and W.
+bool tile256_offsets_ok(int64_t ldq, int64_t ldw, int64_t M, int64_t N, int64_t K);
 
 // Compute units of the current device (cached per device; 256 if it cannot be queried).
 int64_t device_cus();

@@ -422,12 +422,16 @@ int launch_bn(const Dims256& d, int out_dtype, hipStream_t stream) {
 
 }  // namespace
 
+bool tile256_offsets_ok(int64_t ldq, int64_t ldw, int64_t M, int64_t N, int64_t K) {
+  // Tile rows are tracked in 32-bit registers, and byte offsets into q and W in 32-bit lanes.
+  return M <= 0x7fff0000LL && N <= 0x7fff0000LL && (M - 1) * ldq + K <= 0xffffffffLL &&
+         (N - 1) * ldw + K <= 0xffffffffLL;
+}
+
 int launch_tile256(const uint8_t* q, int64_t ldq, const float* as, int64_t as_sk, const uint8_t* w,
                    int64_t ldw, const float* ws, int64_t ws_sn, int64_t ws_sk, void* out, int out_dtype,
                    int64_t ldo, int64_t M, int64_t N, int64_t K, int bn, hipStream_t stream) {
-  // Tile rows are tracked in 32-bit registers, and byte offsets into q and W in 32-bit lanes.
-  if (M > 0x7fff0000LL || N > 0x7fff0000LL || (M - 1) * ldq + K > 0xffffffffLL || (N - 1) * ldw + K > 0xffffffffLL)
-    return MI355X_FP8_ERR_UNSUPPORTED;
+  if (!tile256_offsets_ok(ldq, ldw, M, N, K)) return MI355X_FP8_ERR_UNSUPPORTED;
   const Dims256 d{q, as, w, ws, static_cast<uint16_t*>(out), ldq, as_sk, ldw, ws_sn, ws_sk, ldo, M, N, K / kGroup,
                   (ldo % 4) == 0 && (reinterpret_cast<uintptr_t>(out) % 8) == 0};
   switch (bn) {

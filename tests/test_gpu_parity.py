@@ -381,3 +381,26 @@ def test_reference_gate_every_config_bitwise_and_row_independent(gpu, shape, row
         for row in selected:
             single = fp8.mi355x_fp8_linear(x[row:row + 1], wg, wsg, BLOCK, path="split", gemm_config=config)
             assert bitwise_equal(single, actual[row:row + 1]), (config.name, row)
+
+
+def test_offsets_past_4_gib_use_64_bit_addressing(gpu):
+    """The reference requires 64-bit address arithmetic (tests/test_sm89_fp8_addresses.py:16-58).
+    Here the quantized activations span more than 2^32 bytes: the dispatch must pick a
+    kernel whose offsets reach them, and rows on both sides of the 4 GiB boundary, computed
+    alone, must equal the batched rows bit for bit."""
+
+    k, n = 4096, 256
+    m = (1 << 32) // k + 300  # q (1 byte per element) spans more than 2^32 bytes
+    _note("large offsets", m, k, n)
+    gen = torch.Generator(device=gpu).manual_seed(5)
+    x = torch.randn(m, k, generator=gen, device=gpu, dtype=torch.float32).to(torch.bfloat16)
+    w, ws = make_weights(ModelShape("big_offsets", n, k), 5)
+    wg, wsg = w.to(gpu), ws.to(gpu)
+    out = fp8.mi355x_fp8_linear(x, wg, wsg, BLOCK)
+    boundary = (1 << 32) // k
+    for row in (0, boundary - 1, boundary, m - 1):
+        single = fp8.mi355x_fp8_linear(x[row:row + 1], wg, wsg, BLOCK)
+        assert bitwise_equal(single, out[row:row + 1]), (row, bit_mismatch_details(single, out[row:row + 1]))
+    assert_close_rows(out[m - 4:].cpu(), oracle_linear(x[m - 4:].cpu(), w, ws))
+    del x, out
+    torch.cuda.empty_cache()
