@@ -404,3 +404,32 @@ def test_offsets_past_4_gib_use_64_bit_addressing(gpu):
     assert_close_rows(out[m - 4:].cpu(), oracle_linear(x[m - 4:].cpu(), w, ws))
     del x, out
     torch.cuda.empty_cache()
+
+
+def test_random_shapes_every_config_agrees(gpu):
+    """Seeded random shapes (odd M, N, K, tails and all): every GEMM config gives the bits of
+    the auto dispatch, rows computed alone match, and the result is within tolerance of the
+    oracle."""
+
+    rng = torch.Generator().manual_seed(20261008)
+    for case in range(40):
+        m = int(torch.randint(1, 301, (1,), generator=rng))
+        n = int(torch.randint(1, 700, (1,), generator=rng))
+        k = int(torch.randint(1, 640, (1,), generator=rng))
+        if case % 4 == 0:
+            k = 128 * int(torch.randint(1, 6, (1,), generator=rng))  # 256-row kernel eligible
+        _note("random", case, m, n, k)
+        x = make_activations(m, k, case, torch.bfloat16)
+        w, ws = make_weights(ModelShape("rand", n, k), case)
+        xg, wg, wsg = x.to(gpu), w.to(gpu), ws.to(gpu)
+        auto = fp8.mi355x_fp8_linear(xg, wg, wsg, BLOCK)
+        for config in fp8.GEMM_CONFIGS:
+            if config.name == "tile256" and k % 128:
+                continue
+            forced = fp8.mi355x_fp8_linear(xg, wg, wsg, BLOCK, path="split", gemm_config=config)
+            assert bitwise_equal(auto, forced), (case, m, n, k, config.name, bit_mismatch_details(auto, forced))
+        for row in {0, m // 2, m - 1}:
+            single = fp8.mi355x_fp8_linear(xg[row:row + 1], wg, wsg, BLOCK)
+            assert bitwise_equal(single, auto[row:row + 1]), (case, m, n, k, row)
+        rows = sorted({0, m // 2, m - 1})
+        assert_close_rows(auto[rows].cpu(), oracle_linear(x[rows], w, ws))
