@@ -13,8 +13,8 @@ from _helpers import assert_close_rows, bits16, codes, oracle_linear
 from minillm_amd import merged_projections as mp
 from minillm_amd import mi355x_fp8 as fp8
 from minillm_amd.validation import (
-    SEED, ModelShape, bitwise_equal, make_activations, make_baseline_activations, make_baseline_weights,
-    make_weights,
+    SEED, ModelShape, bit_mismatch_details, bitwise_equal, make_activations, make_baseline_activations,
+    make_baseline_weights, make_weights,
 )
 
 pytestmark = pytest.mark.gpu
@@ -213,3 +213,49 @@ def test_rmsnorm_quant_rejects(gpu):
         fp8.rmsnorm_quant_mi355x_fp8(torch.zeros(2, 130, dtype=torch.bfloat16, device=gpu), w[:130], 1e-6)
     with pytest.raises(ValueError, match="multiple of 4"):
         fp8.rmsnorm_quant_mi355x_fp8(torch.zeros(2, 124, dtype=torch.bfloat16, device=gpu), w[:124], 1e-6)
+
+
+def test_hip_graph_replays_match_eager(gpu):
+    """The ops under HIP-graph capture (the workspace warmed first, as pretune does): decode
+    and prefill linears, the fused SiLU·mul quantizer and the fused RMSNorm quantizer,
+    replayed three times with new inputs copied in eagerly between replays, every replay
+    bitwise equal to the eager calls on the same inputs."""
+
+    shape = ModelShape("kv", 1024, 2560)
+    w, ws = make_baseline_weights(shape, SEED)
+    wg, wsg = w.to(gpu), ws.to(gpu)
+    x_dec = torch.empty(8, 2560, dtype=torch.bfloat16, device=gpu)
+    x_pre = torch.empty(300, 2560, dtype=torch.bfloat16, device=gpu)
+    gate = torch.empty(40, 1024, dtype=torch.bfloat16, device=gpu)
+    up = torch.empty_like(gate)
+    xn = torch.empty(24, 2560, dtype=torch.bfloat16, device=gpu)
+    res = torch.empty_like(xn)
+    nw = (torch.rand(2560, generator=torch.Generator().manual_seed(1)) + 0.5).to(torch.bfloat16).to(gpu)
+
+    def fill(seed):
+        gen = torch.Generator().manual_seed(seed)
+        for t in (x_dec, x_pre, gate, up, xn, res):
+            t.copy_((torch.randn(t.shape, generator=gen) * 3).to(torch.bfloat16))
+
+    def run():
+        return (fp8.mi355x_fp8_linear(x_dec, wg, wsg, [128, 128]), fp8.mi355x_fp8_linear(x_pre, wg, wsg, [128, 128]),
+                *fp8.silu_mul_quant_mi355x_fp8(gate, up), *fp8.rmsnorm_quant_mi355x_fp8(xn, nw, 1e-6, res))
+
+    stream = torch.cuda.Stream()
+    fill(0)
+    with torch.cuda.stream(stream):
+        run()  # sizes this stream's workspace, so the capture allocates nothing of ours
+        stream.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            captured = run()
+    for replay in range(3):
+        fill(100 + replay)
+        torch.cuda.synchronize()
+        with torch.cuda.stream(stream):
+            graph.replay()
+        stream.synchronize()
+        eager = run()
+        torch.cuda.synchronize()
+        for got, want in zip(captured, eager):
+            assert bitwise_equal(got, want), (replay, bit_mismatch_details(got, want))
