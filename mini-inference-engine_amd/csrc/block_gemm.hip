@@ -37,10 +37,10 @@ constexpr int kThreads = 256;  // tile kernel
 // Stream kernel (decode M)
 // ------------------------------------------------------------------------------------
 // One workgroup owns 16*AF consecutive W rows and reads them over the whole of K exactly
-// once.  Its 16 waves take K groups round-robin (wave w: w, w + 16, ...) with the next
-// group's loads in flight, and compute each group's MFMA partial; the partials then meet
-// in LDS, where one thread per output element folds them in K order (below).  16 waves
-// with one group in flight each measured best on the Qwen3-4B shapes.
+// once.  Its 16 waves take K groups round-robin (wave w: w, w + 16, ...) with the next one
+// or two groups' loads in flight, and compute each group's MFMA partial; the partials then
+// meet in LDS, where one thread per output element folds them in K order (below).  16
+// waves per workgroup measured best on the Qwen3-4B shapes.
 constexpr int kStreamWaves = 16;
 // One-round partial buffer limit: two workgroups of 1024 threads share a CU's 160 KiB.
 constexpr size_t kStreamFoldLds = 80 * 1024;
