@@ -10,17 +10,19 @@
 //
 // What differs is the feed: global memory goes straight into LDS with
 // global_load_lds_dwordx4 (no register staging, no ds_write), through a ring of STAGES
-// stages (2 as launched, two workgroups per CU; 3 is kept as a template option), so the
-// loads of K group kb+STAGES-1 are in flight while kb is multiplied.  Each stage
-// holds the W tile (BN rows x 128 B), the activation tile (128 x 128 B) and the 128
+// stages (2 when two workgroups share a CU, 3 when the tiles do not fill the CUs).  Each
+// stage holds the W tile (BN rows x 128 B), the activation tile (128 x 128 B) and the 128
 // activation scales of its K group.  A 64-lane DMA instruction fills 1 KiB of LDS
 // linearly (lane i -> byte 16 i), i.e. 8 rows of 8 16-byte chunks; the XOR swizzle
 // (physical chunk p of row r holds logical chunk p ^ (r & 7)) is applied by choosing each
 // lane's source address, so the MFMA fragment reads (ds_read_b128) are bank-conflict free.
 //
-// The stages are distinct LDS objects and the K loop is unrolled by STAGES, so the
-// compiler can tell the stages apart and does not wait for in-flight DMA before reading
-// the current stage; the waits are explicit (vmcnt) before each workgroup barrier.
+// With one wave per SIMD nothing else hides a wave's LDS reads, so each K step is
+// software-pipelined (k_step): the fragments its first MFMAs need are read during the
+// previous step, each later weight fragment is read while the MFMAs of the one before run,
+// and the workgroup barrier sits between the two parts of a step rather than in front of
+// it.  The K loop is unrolled by STAGES so that every stage index is a compile-time
+// constant.
 //
 // Preconditions (checked by the launcher): K % 128 == 0, W/q base pointers and leading
 // dimensions 16-byte aligned, activation scales K-group-major (as_sm == 1) with row
@@ -59,15 +61,23 @@ __shared__ uint4 stage2[kStageChunks];
 __shared__ uint4 stage3[kStageChunks];
 
 typedef __attribute__((address_space(3))) void lds_void_t;
-typedef const __attribute__((address_space(1))) void global_void_t;
 
+// The DMA instructions are issued through inline assembly.  The compiler then does not
+// track them, so it adds no waits of its own before LDS reads; its alias tracking of LDS
+// DMA is not precise enough for this ring and put vmcnt(0) (every load in flight) in front
+// of fragment reads of a stage whose data had long arrived, and lgkmcnt(0) in front of
+// every MFMA.  All waits for the DMA are the explicit vmcnt waits before the workgroup
+// barriers.  M0 is written without being declared clobbered (it is a reserved register):
+// nothing else in this kernel uses M0, as every LDS DMA of it goes through these helpers.
+// SALU writes of M0 need one wait state before an LDS DMA reads it (the s_nop).
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_void_t*)(p)));
+}
 __device__ __forceinline__ void dma16(const void* src, void* lds_dst) {
-  __builtin_amdgcn_global_load_lds((global_void_t*)(src),
-                                   (lds_void_t*)(lds_dst), 16, 0, 0);
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds_addr(lds_dst)));
 }
 __device__ __forceinline__ void dma4(const void* src, void* lds_dst) {
-  __builtin_amdgcn_global_load_lds((global_void_t*)(src),
-                                   (lds_void_t*)(lds_dst), 4, 0, 0);
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(src), "s"(lds_addr(lds_dst)));
 }
 
 // s_waitcnt with vmcnt = N (6 bits: 3:0 and 15:14) and lgkmcnt = 0, expcnt left at its maximum.
@@ -110,75 +120,138 @@ __device__ __forceinline__ uint4* stage_ptr() {
   else return stage3;
 }
 
+// DMA instruction d (0 .. kDmaPerStage-1) of a stage: W rows, then X rows, then scales.
 template <int BN, int S>
-__device__ __forceinline__ void issue_stage(const DmaSources& src, int64_t kb, int64_t as_sk, int wave, int lane) {
+__device__ __forceinline__ void issue_one(const DmaSources& src, int64_t kb, int64_t as_sk, int wave, int d) {
   using G = DmaGeo<BN>;
   uint4* st = stage_ptr<S>();
   const int64_t koff = kb * kGroup;
-#pragma unroll
-  for (int i = 0; i < G::kNI; ++i) dma16(src.w[i] + koff, st + (i * 4 + wave) * 64);
-#pragma unroll
-  for (int i = 0; i < 4; ++i) dma16(src.x[i] + koff, st + G::kXOff + (i * 4 + wave) * 64);
-  dma4(src.as + kb * as_sk, reinterpret_cast<float*>(st + G::kScaleOff) + wave * 64);
+  if (d < G::kNI) dma16(src.w[d] + koff, st + (d * 4 + wave) * 64);
+  else if (d < G::kNI + 4) dma16(src.x[d - G::kNI] + koff, st + G::kXOff + ((d - G::kNI) * 4 + wave) * 64);
+  else dma4(src.as + kb * as_sk, reinterpret_cast<float*>(st + G::kScaleOff) + wave * 64);
 }
 
 template <int BN, int S>
-__device__ __forceinline__ void compute_stage(v4f (&acc)[DmaGeo<BN>::kNI][4], float wa, float wb, uint32_t use_b,
-                                              int wm, int wn, int r, int g) {
-  using G = DmaGeo<BN>;
-  constexpr int NI = G::kNI;
-  const uint4* st = stage_ptr<S>();
-  const float* sc_lds = reinterpret_cast<const float*>(st + G::kScaleOff);
+__device__ __forceinline__ void issue_stage(const DmaSources& src, int64_t kb, int64_t as_sk, int wave) {
+#pragma unroll
+  for (int d = 0; d < DmaGeo<BN>::kDmaPerStage; ++d) issue_one<BN, S>(src, kb, as_sk, wave, d);
+}
+
+// What the first MFMAs of a K step need, read from its stage one step early: the four
+// activation fragments, the first weight fragment, the activation scales and the weight
+// scales of the K group.
+template <int BN>
+struct StepHead {
+  v8i b[4];
+  v8i a0;
   float as_v[4];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) as_v[j] = sc_lds[wm * 64 + 16 * j + r];  // region wm: rows 64 wm ..
-  v8i a[NI], b[4];
-#pragma unroll
-  for (int i = 0; i < NI; ++i) {
-    const int row = wn * (BN / 2) + 16 * i + r;
-    a[i] = pack_v8i(st[row * 8 + (g ^ (row & 7))], st[row * 8 + ((g + 4) ^ (row & 7))]);
-  }
+  float wa, wb;
+};
+
+template <int BN, int S>
+__device__ __forceinline__ v8i read_a(int i, int wn, int r, int g) {
+  const uint4* st = stage_ptr<S>();
+  const int row = wn * (BN / 2) + 16 * i + r;
+  return pack_v8i(st[row * 8 + (g ^ (row & 7))], st[row * 8 + ((g + 4) ^ (row & 7))]);
+}
+
+template <int BN, int S>
+__device__ __forceinline__ void read_head(StepHead<BN>& h, const DmaSources& src, int64_t kb, int64_t ws_sk,
+                                          int wm, int wn, int r, int g) {
+  using G = DmaGeo<BN>;
+  const uint4* st = stage_ptr<S>();
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int row = wm * 64 + 16 * j + r;
-    b[j] = pack_v8i(st[G::kXOff + row * 8 + (g ^ (row & 7))], st[G::kXOff + row * 8 + ((g + 4) ^ (row & 7))]);
+    h.b[j] = pack_v8i(st[G::kXOff + row * 8 + (g ^ (row & 7))], st[G::kXOff + row * 8 + ((g + 4) ^ (row & 7))]);
   }
-  // 4 NI independent MFMAs into as many partial tiles, each folded into the accumulator
-  // once it is done; the scheduling groups interleave the folds of earlier tiles with the
-  // issue of later MFMAs so that the matrix core never waits on the VALU.
-  v4f p[NI * 4];
+  h.a0 = read_a<BN, S>(0, wn, r, g);
+  const float* sc_lds = reinterpret_cast<const float*>(st + G::kScaleOff);
 #pragma unroll
-  for (int t = 0; t < NI * 4; ++t) p[t] = mfma_16x16x128_e4m3(a[t >> 2], b[t & 3]);
-#pragma unroll
-  for (int t = 0; t < NI * 4; ++t) {
-    const float sc = as_v[t & 3] * ((use_b >> (t >> 2)) & 1 ? wb : wa);
-#pragma unroll
-    for (int v = 0; v < 4; ++v) acc[t >> 2][t & 3][v] = __builtin_fmaf(p[t][v], sc, acc[t >> 2][t & 3][v]);
-  }
-#pragma unroll
-  for (int t = 0; t < NI * 4; ++t) {
-    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
-    __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // four VALU
-  }
+  for (int j = 0; j < 4; ++j) h.as_v[j] = sc_lds[wm * 64 + 16 * j + r];
+  h.wa = src.ws_a[kb * ws_sk];
+  h.wb = src.ws_b[kb * ws_sk];
 }
 
-// One K group: wait for its stage, barrier, refill the stage two groups ahead, multiply.
-// The refill is unconditional (past the end it reloads the last K group into a stage that
-// is no longer read), so every wave always has exactly kDmaPerStage DMA instructions per
-// stage in flight and the waits are static.
+template <int BN>
+__device__ __forceinline__ void fold_group(v4f (&acc)[DmaGeo<BN>::kNI][4], const v4f (&p)[4], const float (&sc)[4],
+                                           int i) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) acc[i][j][v] = __builtin_fmaf(p[j][v], sc[j], acc[i][j][v]);
+}
+
+// One K group kb from stage CUR, whose head h was read during the previous step.
+//   A: weight fragments 0 .. NA-1 are multiplied while fragment i+1 is read;
+//   then the rest of the stage's fragments are read, and the wave waits for them and for
+//   the DMA of the next stage, and passes the workgroup barrier;
+//   B: the next step's head is read from stage CUR+1, stage CUR (now read by every wave)
+//   is refilled with K group kb+STAGES, and the last weight fragments are multiplied.
+// The LDS reads of each part so run behind MFMAs that do not depend on them.  Every
+// output element is still folded once per K group, in K order.
 template <int BN, int STAGES, int CUR>
-__device__ __forceinline__ void k_step(v4f (&acc)[DmaGeo<BN>::kNI][4], const DmaSources& src, int64_t kb, int64_t KB,
-                                       int64_t as_sk, int64_t ws_sk, int wave, int lane, int wm, int wn, int r,
-                                       int g) {
-  constexpr int NXT = (CUR + STAGES - 1) % STAGES;
-  wait_vm_lgkm0<DmaGeo<BN>::kDmaPerStage * (STAGES - 2)>();
-  __builtin_amdgcn_s_barrier();
-  const int64_t ahead = kb + STAGES - 1;
-  issue_stage<BN, NXT>(src, ahead < KB ? ahead : KB - 1, as_sk, wave, lane);
-  if (kb < KB) compute_stage<BN, CUR>(acc, src.ws_a[kb * ws_sk], src.ws_b[kb * ws_sk], src.use_b, wm, wn, r, g);
-  // Keep this step's MFMAs ahead of the next step's wait and barrier, so the matrix core
-  // works through them while the wave waits (measured 6 % faster on o_proj and down).
+__device__ __forceinline__ void k_step(v4f (&acc)[DmaGeo<BN>::kNI][4], StepHead<BN>& h, const DmaSources& src,
+                                       int64_t kb, int64_t KB, int64_t as_sk, int64_t ws_sk, int wave, int wm,
+                                       int wn, int r, int g) {
+  using G = DmaGeo<BN>;
+  constexpr int NI = G::kNI;
+  constexpr int NB = NI >= 4 ? 2 : 1;  // weight fragments multiplied after the barrier
+  constexpr int NA = NI - NB;
+  constexpr int NXT = (CUR + 1) % STAGES;
+  float sa[4], sb[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    sa[j] = h.as_v[j] * h.wa;
+    sb[j] = h.as_v[j] * h.wb;
+  }
+  v8i a[NI];
+  a[0] = h.a0;
+  v4f p[NI][4];
+#pragma unroll
+  for (int i = 0; i < NA; ++i) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) p[i][j] = mfma_16x16x128_e4m3(a[i], h.b[j]);
+    a[i + 1] = read_a<BN, CUR>(i + 1, wn, r, g);
+    if (i > 0) fold_group<BN>(acc, p[i - 1], ((src.use_b >> (i - 1)) & 1) ? sb : sa, i - 1);
+  }
+#pragma unroll
+  for (int i = NA + 1; i < NI; ++i) a[i] = read_a<BN, CUR>(i, wn, r, g);
+  // Per weight fragment of part A: its first MFMA, the two reads of the next fragment
+  // (so that the wait before this MFMA covers only the fragment it needs), then the other
+  // three MFMAs, each followed by folds of the fragment before.
+#pragma unroll
+  for (int i = 0; i < NA; ++i) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
+  }
   __builtin_amdgcn_sched_barrier(0);
+  wait_vm_lgkm0<G::kDmaPerStage * (STAGES - 2)>();
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+  StepHead<BN> nh;
+  read_head<BN, NXT>(nh, src, kb + 1 < KB ? kb + 1 : KB - 1, ws_sk, wm, wn, r, g);
+  const int64_t ahead = kb + STAGES < KB ? kb + STAGES : KB - 1;
+  // The refill's DMA instructions are spread over the MFMAs of part B.
+  constexpr int ND = G::kDmaPerStage, NM = 4 * NB;
+#pragma unroll
+  for (int t = 0; t < NM; ++t) {
+    const int i = NA + t / 4, j = t % 4;
+    p[i][j] = mfma_16x16x128_e4m3(a[i], h.b[j]);
+#pragma unroll
+    for (int d = t * ND / NM; d < (t + 1) * ND / NM; ++d) issue_one<BN, CUR>(src, ahead, as_sk, wave, d);
+    if (j == 3 && i > 0) fold_group<BN>(acc, p[i - 1], ((src.use_b >> (i - 1)) & 1) ? sb : sa, i - 1);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  fold_group<BN>(acc, p[NI - 1], ((src.use_b >> (NI - 1)) & 1) ? sb : sa, NI - 1);
+  __builtin_amdgcn_sched_barrier(0);
+  h = nh;
 }
 
 template <int STAGES, int BN, typename OutT>
@@ -240,15 +313,28 @@ __global__ __launch_bounds__(kDmaThreads, STAGES == 2 ? 2 : 1) void tile_gemm_dm
     for (int j = 0; j < 4; ++j) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
 
   static_assert(STAGES >= 2 && STAGES <= 4, "stages");
-  issue_stage<BN, 0>(src, 0, as_sk, wave, lane);
-  if constexpr (STAGES >= 3) issue_stage<BN, 1>(src, KB > 1 ? 1 : KB - 1, as_sk, wave, lane);
-  if constexpr (STAGES >= 4) issue_stage<BN, 2>(src, KB > 2 ? 2 : KB - 1, as_sk, wave, lane);
-  for (int64_t kb = 0; kb < KB; kb += STAGES) {
-    k_step<BN, STAGES, 0>(acc, src, kb, KB, as_sk, ws_sk, wave, lane, wm, wn, r, g);
-    k_step<BN, STAGES, 1>(acc, src, kb + 1, KB, as_sk, ws_sk, wave, lane, wm, wn, r, g);
-    if constexpr (STAGES >= 3) k_step<BN, STAGES, 2>(acc, src, kb + 2, KB, as_sk, ws_sk, wave, lane, wm, wn, r, g);
-    if constexpr (STAGES >= 4) k_step<BN, STAGES, 3>(acc, src, kb + 3, KB, as_sk, ws_sk, wave, lane, wm, wn, r, g);
+  issue_stage<BN, 0>(src, 0, as_sk, wave);
+  issue_stage<BN, 1>(src, KB > 1 ? 1 : KB - 1, as_sk, wave);
+  if constexpr (STAGES >= 3) issue_stage<BN, 2>(src, KB > 2 ? 2 : KB - 1, as_sk, wave);
+  if constexpr (STAGES >= 4) issue_stage<BN, 3>(src, KB > 3 ? 3 : KB - 1, as_sk, wave);
+  wait_vm_lgkm0<G::kDmaPerStage * (STAGES - 1)>();
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+  StepHead<BN> h;
+  read_head<BN, 0>(h, src, 0, ws_sk, wm, wn, r, g);
+  int64_t kb = 0;
+  for (; kb + STAGES <= KB; kb += STAGES) {
+    k_step<BN, STAGES, 0>(acc, h, src, kb, KB, as_sk, ws_sk, wave, wm, wn, r, g);
+    k_step<BN, STAGES, 1>(acc, h, src, kb + 1, KB, as_sk, ws_sk, wave, wm, wn, r, g);
+    if constexpr (STAGES >= 3) k_step<BN, STAGES, 2>(acc, h, src, kb + 2, KB, as_sk, ws_sk, wave, wm, wn, r, g);
+    if constexpr (STAGES >= 4) k_step<BN, STAGES, 3>(acc, h, src, kb + 3, KB, as_sk, ws_sk, wave, wm, wn, r, g);
   }
+  // The last KB % STAGES groups.
+  if (kb < KB) k_step<BN, STAGES, 0>(acc, h, src, kb, KB, as_sk, ws_sk, wave, wm, wn, r, g);
+  if constexpr (STAGES >= 3)
+    if (kb + 1 < KB) k_step<BN, STAGES, 1>(acc, h, src, kb + 1, KB, as_sk, ws_sk, wave, wm, wn, r, g);
+  if constexpr (STAGES >= 4)
+    if (kb + 2 < KB) k_step<BN, STAGES, 2>(acc, h, src, kb + 2, KB, as_sk, ws_sk, wave, wm, wn, r, g);
   wait_vm_lgkm0<0>();  // no DMA may still target LDS when the workgroup ends
 
   // Lane holds out[m = m0 + 64 wm + 16 j + r][n = n0 + BN/2 wn + 16 i + 4 g + v].
