@@ -73,11 +73,15 @@ typedef __attribute__((address_space(3))) void lds_void_t;
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_void_t*)(p)));
 }
-__device__ __forceinline__ void dma16(const void* src, void* lds_dst) {
-  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds_addr(lds_dst)));
+// 16 (dma16) or 4 (dma4) bytes per lane from base + off: a 64-bit uniform base in SGPRs and
+// a 32-bit per-lane offset, so the K loop spends no VALU on addresses.
+__device__ __forceinline__ void dma16(const void* base, uint32_t off, void* lds_dst) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base),
+               "s"(lds_addr(lds_dst)));
 }
-__device__ __forceinline__ void dma4(const void* src, void* lds_dst) {
-  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(src), "s"(lds_addr(lds_dst)));
+__device__ __forceinline__ void dma4(const void* base, uint32_t off, void* lds_dst) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1" ::"v"(off), "s"(base),
+               "s"(lds_addr(lds_dst)));
 }
 
 // s_waitcnt with vmcnt = N (6 bits: 3:0 and 15:14) and lgkmcnt = 0, expcnt left at its maximum.
@@ -104,9 +108,12 @@ __device__ __forceinline__ void tile_of_dma(int64_t pid, int64_t tiles_m, int64_
 }
 
 struct DmaSources {
-  const uint8_t* w[5];
-  const uint8_t* x[4];
-  const float* as;
+  const uint8_t* w;   // W row n0 of the tile
+  const uint8_t* x;   // activation row m0 of the tile
+  const float* as;    // activation scale of row m0, K group 0
+  uint32_t woff[5];   // per-lane byte offsets from w of the W rows each DMA instruction fills
+  uint32_t xoff[4];   // the same for the activation rows, from x
+  uint32_t soff;      // per-lane byte offset from as of the scale this lane stages
   const float* ws_a;  // weight scales of the (at most two) 128-column blocks the wave's columns touch
   const float* ws_b;
   uint32_t use_b;     // bit i: the wave's column tile i lies in block ws_b
@@ -126,9 +133,9 @@ __device__ __forceinline__ void issue_one(const DmaSources& src, int64_t kb, int
   using G = DmaGeo<BN>;
   uint4* st = stage_ptr<S>();
   const int64_t koff = kb * kGroup;
-  if (d < G::kNI) dma16(src.w[d] + koff, st + (d * 4 + wave) * 64);
-  else if (d < G::kNI + 4) dma16(src.x[d - G::kNI] + koff, st + G::kXOff + ((d - G::kNI) * 4 + wave) * 64);
-  else dma4(src.as + kb * as_sk, reinterpret_cast<float*>(st + G::kScaleOff) + wave * 64);
+  if (d < G::kNI) dma16(src.w + koff, src.woff[d], st + (d * 4 + wave) * 64);
+  else if (d < G::kNI + 4) dma16(src.x + koff, src.xoff[d - G::kNI], st + G::kXOff + ((d - G::kNI) * 4 + wave) * 64);
+  else dma4(src.as + kb * as_sk, src.soff, reinterpret_cast<float*>(st + G::kScaleOff) + wave * 64);
 }
 
 template <int BN, int S>
@@ -173,9 +180,19 @@ __device__ __forceinline__ void read_head(StepHead<BN>& h, const DmaSources& src
   h.wb = src.ws_b[kb * ws_sk];
 }
 
+// Folds column tile i's partials into the accumulator: acc = fma(p, as * ws, acc), ws being
+// the scale of the 128-column weight block the tile lies in.  Only BN = 160 lets a wave's
+// tiles straddle two blocks: there the tile's block scale is picked on the scalar unit and
+// its four scale products formed here; otherwise all tiles share the step's products sa.
 template <int BN>
-__device__ __forceinline__ void fold_group(v4f (&acc)[DmaGeo<BN>::kNI][4], const v4f (&p)[4], const float (&sc)[4],
-                                           int i) {
+__device__ __forceinline__ void fold_tile(v4f (&acc)[DmaGeo<BN>::kNI][4], const v4f (&p)[4], const StepHead<BN>& h,
+                                          const float (&sa)[4], uint32_t use_b, int i) {
+  float sc[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    if constexpr (BN == 160) sc[j] = h.as_v[j] * (((use_b >> i) & 1) ? h.wb : h.wa);
+    else sc[j] = sa[j];
+  }
 #pragma unroll
   for (int j = 0; j < 4; ++j)
 #pragma unroll
@@ -199,12 +216,9 @@ __device__ __forceinline__ void k_step(v4f (&acc)[DmaGeo<BN>::kNI][4], StepHead<
   constexpr int NB = NI >= 4 ? 2 : 1;  // weight fragments multiplied after the barrier
   constexpr int NA = NI - NB;
   constexpr int NXT = (CUR + 1) % STAGES;
-  float sa[4], sb[4];
+  float sa[4];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    sa[j] = h.as_v[j] * h.wa;
-    sb[j] = h.as_v[j] * h.wb;
-  }
+  for (int j = 0; j < 4; ++j) sa[j] = h.as_v[j] * h.wa;
   v8i a[NI];
   a[0] = h.a0;
   v4f p[NI][4];
@@ -213,7 +227,7 @@ __device__ __forceinline__ void k_step(v4f (&acc)[DmaGeo<BN>::kNI][4], StepHead<
 #pragma unroll
     for (int j = 0; j < 4; ++j) p[i][j] = mfma_16x16x128_e4m3(a[i], h.b[j]);
     a[i + 1] = read_a<BN, CUR>(i + 1, wn, r, g);
-    if (i > 0) fold_group<BN>(acc, p[i - 1], ((src.use_b >> (i - 1)) & 1) ? sb : sa, i - 1);
+    if (i > 0) fold_tile<BN>(acc, p[i - 1], h, sa, src.use_b, i - 1);
   }
 #pragma unroll
   for (int i = NA + 1; i < NI; ++i) a[i] = read_a<BN, CUR>(i, wn, r, g);
@@ -246,10 +260,10 @@ __device__ __forceinline__ void k_step(v4f (&acc)[DmaGeo<BN>::kNI][4], StepHead<
     p[i][j] = mfma_16x16x128_e4m3(a[i], h.b[j]);
 #pragma unroll
     for (int d = t * ND / NM; d < (t + 1) * ND / NM; ++d) issue_one<BN, CUR>(src, ahead, as_sk, wave, d);
-    if (j == 3 && i > 0) fold_group<BN>(acc, p[i - 1], ((src.use_b >> (i - 1)) & 1) ? sb : sa, i - 1);
+    if (j == 3 && i > 0) fold_tile<BN>(acc, p[i - 1], h, sa, src.use_b, i - 1);
     __builtin_amdgcn_sched_barrier(0);
   }
-  fold_group<BN>(acc, p[NI - 1], ((src.use_b >> (NI - 1)) & 1) ? sb : sa, NI - 1);
+  fold_tile<BN>(acc, p[NI - 1], h, sa, src.use_b, NI - 1);
   __builtin_amdgcn_sched_barrier(0);
   h = nh;
 }
@@ -275,21 +289,24 @@ __global__ __launch_bounds__(kDmaThreads, STAGES == 2 ? 2 : 1) void tile_gemm_dm
   const int64_t n0 = tn * BN;
 
   DmaSources src;
+  src.w = w + n0 * ldw;
+  src.x = q + m0 * ldq;
+  src.as = as + m0;
 #pragma unroll
   for (int i = 0; i < 5; ++i) {
     const int rr = (i * 4 + wave) * 8 + (lane >> 3);
     const int c = (lane & 7) ^ (rr & 7);
-    const int64_t wrow = (n0 + rr) < N ? (n0 + rr) : (N - 1);
-    src.w[i] = i < NI ? w + wrow * ldw + 16 * c : w;
+    const int64_t wrow = (n0 + rr) < N ? rr : (N - 1 - n0);
+    src.woff[i] = static_cast<uint32_t>(wrow * ldw + 16 * c);
     if (i < 4) {
-      const int64_t xrow = (m0 + rr) < M ? (m0 + rr) : (M - 1);
-      src.x[i] = q + xrow * ldq + 16 * c;
+      const int64_t xrow = (m0 + rr) < M ? rr : (M - 1 - m0);
+      src.xoff[i] = static_cast<uint32_t>(xrow * ldq + 16 * c);
     }
   }
   {
     // Wave w stages the scales of tile rows 64 (w & 1) .. +63 (waves 2, 3 duplicate 0, 1).
-    const int64_t srow = m0 + (wave & 1) * 64 + lane;
-    src.as = as + (srow < M ? srow : M - 1);
+    const int64_t srow = (wave & 1) * 64 + lane;
+    src.soff = static_cast<uint32_t>(4 * (m0 + srow < M ? srow : M - 1 - m0));
   }
   {
     // The wave's columns [nw, nw + BN/2) touch at most two 128-column weight-scale blocks.
@@ -365,6 +382,9 @@ __global__ __launch_bounds__(kDmaThreads, STAGES == 2 ? 2 : 1) void tile_gemm_dm
 
 bool tile_dma_supported(const uint8_t* q, int64_t ldq, int64_t as_sm, int64_t as_sk, const uint8_t* w,
                         int64_t ldw, int64_t M, int64_t K) {
+  // The per-lane DMA offsets within a tile are 32-bit (the row bases are 64-bit).
+  constexpr int64_t kMaxOff = 0xffffffffLL - kGroup;
+  if (ldq > kMaxOff / (kTileRows - 1) || ldw > kMaxOff / (kMaxBN - 1)) return false;
   return K % kGroup == 0 && ldq % 16 == 0 && ldw % 16 == 0 && reinterpret_cast<uintptr_t>(q) % 16 == 0 &&
          reinterpret_cast<uintptr_t>(w) % 16 == 0 && as_sm == 1 && as_sk >= M;
 }
