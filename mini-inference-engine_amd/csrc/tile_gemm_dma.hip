@@ -26,8 +26,9 @@
 //
 // Preconditions (checked by the launcher): K % 128 == 0, W/q base pointers and leading
 // dimensions 16-byte aligned, activation scales K-group-major (as_sm == 1) with row
-// length as_sk >= M.  Out-of-range tile rows read the last valid row (finite data whose
-// outputs are never stored).
+// length as_sk >= M, row strides below 2^32 / 159 bytes (W) and 2^32 / 127 bytes (q), so that
+// the 32-bit per-lane offsets within a tile reach every row.  Out-of-range tile rows read the
+// last valid row (finite data whose outputs are never stored).
 #include "fp8_abi_internal.h"
 #include "fp8_common.h"
 

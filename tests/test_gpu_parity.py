@@ -406,6 +406,31 @@ def test_offsets_past_4_gib_use_64_bit_addressing(gpu):
     torch.cuda.empty_cache()
 
 
+def test_weight_row_stride_past_32_bit_lane_offsets(gpu):
+    """The LDS-DMA kernels address a tile's rows as a 64-bit base plus 32-bit per-lane
+    offsets, which a weight row stride of more than 2^32 / 160 bytes would overflow.  Such a
+    weight (a row-strided view into a larger buffer) must take a kernel whose offsets reach
+    it and give the bits of the same weight stored contiguously."""
+
+    m, n, k = 300, 3, 256
+    ldw = 27_000_000  # (160 - 1) * ldw > 2^32, a multiple of 16
+    _note("weight stride", m, n, k, ldw)
+    x = make_activations(m, k, 11, torch.bfloat16)
+    w, ws = make_weights(ModelShape("strided_w", n, k), 11)
+    xg, wg, wsg = x.to(gpu), w.to(gpu), ws.to(gpu)
+    storage = torch.zeros((n - 1) * ldw + k, dtype=torch.uint8, device=gpu)
+    strided = storage.as_strided((n, k), (ldw, 1))
+    strided.copy_(wg.view(torch.uint8))
+    w_strided = strided.view(torch.float8_e4m3fn)
+    assert w_strided.stride() == (ldw, 1)
+    out = fp8.mi355x_fp8_linear(xg, w_strided, wsg, BLOCK)
+    ref = fp8.mi355x_fp8_linear(xg, wg, wsg, BLOCK)
+    assert bitwise_equal(out, ref), bit_mismatch_details(out, ref)
+    assert_close_rows(out.cpu(), oracle_linear(x, w, ws))
+    del storage
+    torch.cuda.empty_cache()
+
+
 def test_random_shapes_every_config_agrees(gpu):
     """Seeded random shapes (odd M, N, K, tails and all): every GEMM config gives the bits of
     the auto dispatch, rows computed alone match, and the result is within tolerance of the
