@@ -64,4 +64,12 @@ int64_t device_cus();
 
 inline size_t align256(size_t v) { return (v + 255) & ~static_cast<size_t>(255); }
 
+// How a prefill kernel may store its 16-bit output rows: 2 in 16-byte pieces through LDS
+// (16-byte aligned rows), 1 in 8-byte pieces, 0 one element at a time.
+inline int out_vec_mode(const void* out, int64_t ldo) {
+  const uintptr_t p = reinterpret_cast<uintptr_t>(out);
+  if (ldo % 8 == 0 && p % 16 == 0) return 2;
+  return (ldo % 4 == 0 && p % 8 == 0) ? 1 : 0;
+}
+
 }  // namespace mi355x

@@ -50,6 +50,30 @@ template <> struct OutCvt<f16_t> {
   __device__ static uint16_t cvt(float f) { return f32_to_f16_bits(f); }
 };
 
+// Prefill epilogue through LDS.  Each lane first writes its 4-column pieces of the output
+// tile into LDS (row-major, a row of BN halfwords at pitch staged_pitch<BN>()), then every
+// row goes out in 16-byte pieces with consecutive lanes on consecutive pieces, as
+// non-temporal stores.  Full-line streaming stores leave no dirty output lines in L2 for the
+// end-of-kernel write-back, which otherwise runs after the last tile's loop; scattered 8-byte
+// stores (non-temporal or not) measured slower.
+// A row pitch of BN halfwords when BN is a multiple of 128, with the 16-byte pieces of row r
+// XOR-swizzled by r & 15, else BN + 8 halfwords: either way the 16 rows a wave writes at once
+// and the 16-byte reads land in distinct banks.
+template <int BN>
+__device__ constexpr int staged_pitch() {
+  return BN % 128 == 0 ? BN : BN + 8;
+}
+// Halfword index of column col (a multiple of 4) of staged row row.
+template <int BN>
+__device__ __forceinline__ int staged_index(int row, int col) {
+  const int piece = BN % 128 == 0 ? ((col >> 3) ^ (row & 15)) : (col >> 3);
+  return row * staged_pitch<BN>() + piece * 8 + (col & 7);
+}
+__device__ __forceinline__ void store16_nt(uint16_t* dst, uint4 v) {
+  typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+  __builtin_nontemporal_store(u32x4{v.x, v.y, v.z, v.w}, reinterpret_cast<u32x4*>(dst));
+}
+
 // fp32 rounded to the nearest bf16 (ties to even), returned as fp32.
 __device__ __forceinline__ float round_bf16(float f) {
   return __uint_as_float(static_cast<uint32_t>(f32_to_bf16_bits(f)) << 16);

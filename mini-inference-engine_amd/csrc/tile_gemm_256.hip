@@ -268,7 +268,7 @@ struct Dims256 {
   const float* ws;
   uint16_t* out;
   int64_t ldq, as_sk, ldw, ws_sn, ws_sk, ldo, M, N, KB;
-  int vec_out;
+  int vec_out;  // out_vec_mode(out, ldo)
 };
 
 template <int BN>
@@ -387,6 +387,46 @@ __device__ __forceinline__ void store_tile(const v4f (&acc)[Geo<BN>::kNI][4], co
   }
 }
 
+// The epilogue through LDS (staged_index, fp8_common.h): rows 0-127 of the tile in ring stage
+// 0, rows 128-255 in stage 1.  Needs 16-byte aligned output rows (vec_out == 2).
+template <int BN, int NS, typename OutT>
+__device__ __forceinline__ void store_tile_lds(const v4f (&acc)[Geo<BN>::kNI][4], const Dims256& d, int64_t m0,
+                                               int64_t n0, int wm, int wn, int r, int g, int tid) {
+  uint16_t* r0 = reinterpret_cast<uint16_t*>(stage256<NS, 0>());
+  uint16_t* r1 = reinterpret_cast<uint16_t*>(stage256<NS, 1>());
+  static_assert(128 * staged_pitch<BN>() * 2 <= (NS == 2 ? kStageU4 : kStage3U4) * 16, "staged rows fit a stage");
+  __syncthreads();  // every wave is done with the ring
+  uint16_t* reg = wm < 2 ? r0 : r1;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+#pragma unroll
+    for (int i = 0; i < Geo<BN>::kNI; ++i) {
+      uint16_t h[4];
+#pragma unroll
+      for (int v = 0; v < 4; ++v) h[v] = OutCvt<OutT>::cvt(acc[i][j][v]);
+      *reinterpret_cast<uint2*>(reg + staged_index<BN>((wm & 1) * 64 + 16 * j + r, wn * (BN / 2) + 16 * i + 4 * g)) =
+          make_uint2(h[0] | (static_cast<uint32_t>(h[1]) << 16), h[2] | (static_cast<uint32_t>(h[3]) << 16));
+    }
+  }
+  __syncthreads();
+  constexpr int C = BN / 8;  // 16-byte pieces per row
+#pragma unroll 4
+  for (int idx = tid; idx < kRowsT * C; idx += kT256Threads) {
+    const int row = idx / C, c = idx - (idx / C) * C;
+    const int64_t m = m0 + row, n = n0 + 8 * c;
+    const uint4 val = *reinterpret_cast<const uint4*>((row < 128 ? r0 : r1) + staged_index<BN>(row & 127, 8 * c));
+    if (m >= d.M) continue;
+    uint16_t* dst = d.out + m * d.ldo + n;
+    if (n + 8 <= d.N) {
+      store16_nt(dst, val);
+    } else {
+      const uint16_t* hv = reinterpret_cast<const uint16_t*>(&val);
+      for (int v = 0; v < 8; ++v)
+        if (n + v < d.N) dst[v] = hv[v];
+    }
+  }
+}
+
 template <int BN, int NS, typename OutT>
 __global__ __launch_bounds__(kT256Threads, 2) void tile256_gemm_kernel(Dims256 d, int64_t tiles_m, int64_t tiles_n) {
   const int tid = threadIdx.x;
@@ -404,7 +444,8 @@ __global__ __launch_bounds__(kT256Threads, 2) void tile256_gemm_kernel(Dims256 d
   v4f acc[Geo<BN>::kNI][4];
   run_k<BN, NS>(acc, src, d, 0, d.KB, wave, wm, wn, r, g);
   __builtin_amdgcn_s_waitcnt(0x70);  // no DMA may still target LDS when the workgroup ends
-  store_tile<BN, OutT>(acc, d, tm * kRowsT, tn * BN, wm, wn, r, g);
+  if (d.vec_out == 2) store_tile_lds<BN, NS, OutT>(acc, d, tm * kRowsT, tn * BN, wm, wn, r, g, tid);
+  else store_tile<BN, OutT>(acc, d, tm * kRowsT, tn * BN, wm, wn, r, g);
 }
 
 template <int BN, int NS>
@@ -433,7 +474,7 @@ int launch_tile256(const uint8_t* q, int64_t ldq, const float* as, int64_t as_sk
                    int64_t ldo, int64_t M, int64_t N, int64_t K, int bn, hipStream_t stream) {
   if (!tile256_offsets_ok(ldq, ldw, M, N, K)) return MI355X_FP8_ERR_UNSUPPORTED;
   const Dims256 d{q, as, w, ws, static_cast<uint16_t*>(out), ldq, as_sk, ldw, ws_sn, ws_sk, ldo, M, N, K / kGroup,
-                  (ldo % 4) == 0 && (reinterpret_cast<uintptr_t>(out) % 8) == 0};
+                  out_vec_mode(out, ldo)};
   switch (bn) {
     case 256: return launch_bn<256, 2>(d, out_dtype, stream);
     case 224: return launch_bn<224, 2>(d, out_dtype, stream);

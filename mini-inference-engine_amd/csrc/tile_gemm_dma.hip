@@ -355,6 +355,45 @@ __global__ __launch_bounds__(kDmaThreads, STAGES == 2 ? 2 : 1) void tile_gemm_dm
     if (kb + 2 < KB) k_step<BN, STAGES, 2>(acc, h, src, kb + 2, KB, as_sk, ws_sk, wave, wm, wn, r, g);
   wait_vm_lgkm0<0>();  // no DMA may still target LDS when the workgroup ends
 
+  if (vec_out == 2) {
+    // Through LDS (staged_index, fp8_common.h): tile rows 0-63 in stage0, 64-127 in stage1.
+    static_assert(64 * staged_pitch<BN>() * 2 <= kStageChunks * 16, "staged rows fit a stage");
+    __syncthreads();  // every wave is done with the ring
+    uint16_t* reg = reinterpret_cast<uint16_t*>(wm == 0 ? stage0 : stage1);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+#pragma unroll
+      for (int i = 0; i < NI; ++i) {
+        uint16_t h[4];
+#pragma unroll
+        for (int v = 0; v < 4; ++v) h[v] = OutCvt<OutT>::cvt(acc[i][j][v]);
+        *reinterpret_cast<uint2*>(reg + staged_index<BN>(16 * j + r, wn * (BN / 2) + 16 * i + 4 * g)) =
+            make_uint2(h[0] | (static_cast<uint32_t>(h[1]) << 16), h[2] | (static_cast<uint32_t>(h[3]) << 16));
+      }
+    }
+    __syncthreads();
+    constexpr int C = BN / 8;  // 16-byte pieces per row
+    static_assert((kTileRows * C) % kDmaThreads == 0, "whole passes");
+#pragma unroll
+    for (int it = 0; it < kTileRows * C / kDmaThreads; ++it) {
+      const int idx = tid + it * kDmaThreads;
+      const int row = idx / C, c = idx - (idx / C) * C;
+      const int64_t m = m0 + row, n = n0 + 8 * c;
+      const uint16_t* reg_r = reinterpret_cast<const uint16_t*>(row < 64 ? stage0 : stage1);
+      const uint4 val = *reinterpret_cast<const uint4*>(reg_r + staged_index<BN>(row & 63, 8 * c));
+      if (m >= M) continue;
+      uint16_t* dst = out + m * ldo + n;
+      if (n + 8 <= N) {
+        store16_nt(dst, val);
+      } else {
+        const uint16_t* hv = reinterpret_cast<const uint16_t*>(&val);
+        for (int v = 0; v < 8; ++v)
+          if (n + v < N) dst[v] = hv[v];
+      }
+    }
+    return;
+  }
+
   // Lane holds out[m = m0 + 64 wm + 16 j + r][n = n0 + BN/2 wn + 16 i + 4 g + v].
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
@@ -397,7 +436,7 @@ int launch_tile_dma(const uint8_t* q, int64_t ldq, const float* as, int64_t as_s
   const int64_t tiles_m = (M + kTileRows - 1) / kTileRows;
   const int64_t tiles_n = (N + bn - 1) / bn;
   if (tiles_m * tiles_n > 0x7fffffffLL) return MI355X_FP8_ERR_UNSUPPORTED;
-  const int vec_out = (ldo % 4) == 0 && (reinterpret_cast<uintptr_t>(out) % 8) == 0;
+  const int vec_out = out_vec_mode(out, ldo);
   dim3 grid(static_cast<unsigned>(tiles_m * tiles_n));
   uint16_t* o = static_cast<uint16_t*>(out);
   // Two stages (76 KiB, room for the 160-wide W tile) let two workgroups share a CU.
