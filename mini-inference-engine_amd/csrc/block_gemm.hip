@@ -467,11 +467,11 @@ int64_t device_cus() {
 // their steps shorter.  Time of one full wave of tiles over K = 2560 on MI355X (µs, every
 // CU busy; the DMA kernel's second figure is for two workgroups per CU, the layout it
 // takes when the tiles outnumber the CUs):
-//   256 x 256 / 224 / 192 (two stages)   47.7  45.3  39.8
-//   256 x 160 / 128 (three stages)       35.4  29.9
-//   128 x 160 / 128 / 64 (three stages)  22.7  19.0  13.2   (two per CU: 44.1  31.2  21.8)
+//   256 x 256 / 224 / 192 (two stages)   46.5  42.4  37.4
+//   256 x 160 / 128 (three stages)       33.5  28.0
+//   128 x 160 / 128 / 64 (three stages)  21.4  17.5  12.5   (two per CU: 33.5  28.5  20.4)
 // A last, partly filled wave costs 0.7 + 0.3 x its fill of a full one (a half-filled wave
-// measured 0.79-0.97).  Every kernel gives the same bits, so the choice may follow M.
+// measured 0.75-0.98).  Every kernel gives the same bits, so the choice may follow M.
 #ifndef MI355X_PREFILL_POLICY
 #define MI355X_PREFILL_POLICY 0  // 0: cost model, 1: always 256-row, 2: always 128-row
 #endif
@@ -482,8 +482,8 @@ struct TileVariant {
   double wave_two;  // µs per full wave of two workgroups per CU (0: not used)
 };
 constexpr TileVariant kTileVariants[] = {
-    {256, 256, 47.7, 0.0}, {256, 224, 45.3, 0.0}, {256, 192, 39.8, 0.0}, {256, 160, 35.4, 0.0},
-    {256, 128, 29.9, 0.0}, {128, 160, 22.7, 44.1}, {128, 128, 19.0, 31.2}, {128, 64, 13.2, 21.8},
+    {256, 256, 46.5, 0.0}, {256, 224, 42.4, 0.0}, {256, 192, 37.4, 0.0}, {256, 160, 33.5, 0.0},
+    {256, 128, 28.0, 0.0}, {128, 160, 21.4, 33.5}, {128, 128, 17.5, 28.5}, {128, 64, 12.5, 20.4},
 };
 
 double waves_cost(int64_t tiles, int64_t slots, double wave) {
