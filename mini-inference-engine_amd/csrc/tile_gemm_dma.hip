@@ -39,6 +39,9 @@ constexpr int kDmaThreads = 256;
 #ifndef MI355X_DMA_STAGES_FEW
 #define MI355X_DMA_STAGES_FEW 3  // ring depth when the tiles do not exceed the CUs
 #endif
+#ifndef MI355X_DMA_STAGES_FEW_NARROW
+#define MI355X_DMA_STAGES_FEW_NARROW 4  // the same for the 64-wide tiles
+#endif
 #ifndef MI355X_DMA_STAGES_MANY
 #define MI355X_DMA_STAGES_MANY 2  // ring depth otherwise (two workgroups per CU)
 #endif
@@ -441,21 +444,23 @@ int launch_tile_dma(const uint8_t* q, int64_t ldq, const float* as, int64_t as_s
   uint16_t* o = static_cast<uint16_t*>(out);
   // Two stages (76 KiB, room for the 160-wide W tile) let two workgroups share a CU.
   // When the tiles do not fill the CUs anyway, each K step waits on its DMA round trip,
-  // so a deeper ring (one workgroup per CU) keeps more K groups in flight.
-  const int stages = tiles_m * tiles_n <= device_cus() ? MI355X_DMA_STAGES_FEW : MI355X_DMA_STAGES_MANY;
+  // so a deeper ring (one workgroup per CU) keeps more K groups in flight: three stages,
+  // four for the 64-wide tiles, whose short steps wait longest (measured on o_proj and down
+  // at 256 and 536 rows; four stages for the wider tiles measured slower).
+  const bool few = tiles_m * tiles_n <= device_cus();
 #define MI355X_DMA_ARGS q, ldq, as, as_sk, w, ldw, ws, ws_sn, ws_sk, o, ldo, M, N, K / kGroup, tiles_m, tiles_n, vec_out
 #define MI355X_DMA_LAUNCH(ST, BN)                                                                                  \
   (out_dtype == kBF16 ? tile_gemm_dma_kernel<ST, BN, bf16_t><<<grid, kDmaThreads, 0, stream>>>(MI355X_DMA_ARGS) \
                       : tile_gemm_dma_kernel<ST, BN, f16_t><<<grid, kDmaThreads, 0, stream>>>(MI355X_DMA_ARGS))
-#define MI355X_DMA_BY_BN(ST)                \
-  do {                                      \
-    if (bn == 160) MI355X_DMA_LAUNCH(ST, 160); \
-    else if (bn == 64) MI355X_DMA_LAUNCH(ST, 64); \
-    else MI355X_DMA_LAUNCH(ST, 128);        \
-  } while (0)
-  if (stages == MI355X_DMA_STAGES_MANY) MI355X_DMA_BY_BN(MI355X_DMA_STAGES_MANY);
-  else MI355X_DMA_BY_BN(MI355X_DMA_STAGES_FEW);
-#undef MI355X_DMA_BY_BN
+  if (!few) {
+    if (bn == 160) MI355X_DMA_LAUNCH(MI355X_DMA_STAGES_MANY, 160);
+    else if (bn == 64) MI355X_DMA_LAUNCH(MI355X_DMA_STAGES_MANY, 64);
+    else MI355X_DMA_LAUNCH(MI355X_DMA_STAGES_MANY, 128);
+  } else {
+    if (bn == 160) MI355X_DMA_LAUNCH(MI355X_DMA_STAGES_FEW, 160);
+    else if (bn == 64) MI355X_DMA_LAUNCH(MI355X_DMA_STAGES_FEW_NARROW, 64);
+    else MI355X_DMA_LAUNCH(MI355X_DMA_STAGES_FEW, 128);
+  }
 #undef MI355X_DMA_LAUNCH
 #undef MI355X_DMA_ARGS
   return hipGetLastError() == hipSuccess ? MI355X_FP8_OK : MI355X_FP8_ERR_LAUNCH;
