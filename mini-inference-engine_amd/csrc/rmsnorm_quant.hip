@@ -101,7 +101,10 @@ __global__ __launch_bounds__(64 * kRnqWavesPerBlock) void rmsnorm_quant_kernel(
               sw[i] = lo | (hi << 16);
             }
             v = make_uint4(sw[0], sw[1], sw[2], sw[3]);
-            *reinterpret_cast<uint4*>(res_out + m * ldro + 8 * c) = v;
+            // Non-temporal: the next reader of the residual stream is a later layer, and
+            // full-line streaming stores leave no dirty lines for the end-of-kernel
+            // write-back (measured 12.6 -> 11.2 us at 2048 rows).
+            store16_nt(res_out + m * ldro + 8 * c, v);
           }
           *reinterpret_cast<uint4*>(row + 8 * c) = v;
         }
