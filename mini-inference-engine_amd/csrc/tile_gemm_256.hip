@@ -28,7 +28,10 @@
 // p ^ (r & 7)) is applied through each lane's source address, so fragment reads
 // (ds_read_b128) are bank-conflict free.  The stages are distinct LDS objects and the K
 // loop is unrolled by two, so the compiler never waits for in-flight DMA before reading
-// the current stage; the waits are explicit.
+// the current stage; the waits are explicit.  (BN = 160 and 128 use a three-stage ring.)
+//
+// The output tile leaves through LDS as full-row 16-byte non-temporal stores when the output
+// rows are 16-byte aligned (store_tile_lds), else straight from the registers (store_tile).
 //
 // Preconditions (checked by the launcher): K % 128 == 0, q/W 16-byte aligned with
 // leading dimensions multiple of 16, scales K-group-major (as_sm == 1, as_sk >= M), byte

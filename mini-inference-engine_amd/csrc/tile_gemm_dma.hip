@@ -10,9 +10,9 @@
 //
 // What differs is the feed: global memory goes straight into LDS with
 // global_load_lds_dwordx4 (no register staging, no ds_write), through a ring of STAGES
-// stages (2 when two workgroups share a CU, 3 when the tiles do not fill the CUs).  Each
-// stage holds the W tile (BN rows x 128 B), the activation tile (128 x 128 B) and the 128
-// activation scales of its K group.  A 64-lane DMA instruction fills 1 KiB of LDS
+// stages (2 when two workgroups share a CU; when the tiles do not fill the CUs, 3, or 4 for
+// BN = 64).  Each stage holds the W tile (BN rows x 128 B), the activation tile
+// (128 x 128 B) and the 128 activation scales of its K group.  A 64-lane DMA instruction fills 1 KiB of LDS
 // linearly (lane i -> byte 16 i), i.e. 8 rows of 8 16-byte chunks; the XOR swizzle
 // (physical chunk p of row r holds logical chunk p ^ (r & 7)) is applied by choosing each
 // lane's source address, so the MFMA fragment reads (ds_read_b128) are bank-conflict free.
@@ -23,6 +23,9 @@
 // and the workgroup barrier sits between the two parts of a step rather than in front of
 // it.  The K loop is unrolled by STAGES so that every stage index is a compile-time
 // constant.
+//
+// The output tile leaves through LDS as full-row 16-byte non-temporal stores when the output
+// rows are 16-byte aligned (staged_index, fp8_common.h), else straight from the registers.
 //
 // Preconditions (checked by the launcher): K % 128 == 0, W/q base pointers and leading
 // dimensions 16-byte aligned, activation scales K-group-major (as_sm == 1) with row
