@@ -207,6 +207,33 @@ def test_gemm_entry_kgroup_scale_layout(gpu, config, shape, rows):
     assert_close_rows(out, oracle_gemm(q.cpu(), s_row.cpu(), w, ws))
 
 
+@pytest.mark.parametrize("config", fp8.GEMM_CONFIGS[1:], ids=lambda c: c.name)
+@pytest.mark.parametrize("rows,n", [(300, 320), (200, 1000), (129, 2560)])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_prefill_output_views_every_store_mode(gpu, config, rows, n, dtype):
+    """The prefill kernels store a tile three ways, by the output rows' alignment: through
+    LDS as 16-byte pieces (16-byte aligned rows), 8-byte pieces, or one element at a time.
+    Row-strided output views that select each mode give the bits of a contiguous output."""
+
+    k = 512
+    _note("output views", config.name, rows, n, dtype)
+    x = make_activations(rows, k, 17)
+    w, ws = make_weights(ModelShape("views", n, k), 17)
+    wg, wsg = w.to(gpu), ws.to(gpu)
+    q, s = fp8.quantize_mi355x_fp8_activation(x.to(gpu), scale_layout="kgroup")
+    ref = torch.empty((rows, n), dtype=dtype, device=gpu)
+    fp8.launch_block_gemm(q, wg, ref, s, wsg, config)
+    # (column offset, row pitch): 16-byte aligned rows, 8-byte aligned rows, 2-byte aligned rows
+    for col, pitch in ((8, n + 16), (4, n + 8), (1, n + 3)):
+        big = torch.full((rows, pitch), float("nan"), dtype=dtype, device=gpu)
+        view = big[:, col:col + n]
+        fp8.launch_block_gemm(q, wg, view, s, wsg, config)
+        assert bitwise_equal(view, ref), (col, pitch, bit_mismatch_details(view, ref))
+        assert torch.isnan(big[:, :col]).all() and torch.isnan(big[:, col + n:]).all(), (col, pitch)
+    if dtype == torch.bfloat16:
+        assert_close_rows(ref, oracle_gemm(q.cpu(), s.contiguous().cpu(), w, ws))
+
+
 @pytest.mark.parametrize("output_dtype", [torch.bfloat16, torch.float16])
 def test_bias_output_dtype_and_flattened_input(gpu, output_dtype):
     x = make_activations(6, 259, 42).reshape(2, 3, 259)
