@@ -86,13 +86,31 @@ def pretune_row_buckets(max_tokens: int) -> tuple[int, ...]:
     return tuple(1 << i for i in range(m_bucket(max(1, max_tokens)).bit_length()))
 
 
+_ARCH_OK: dict[int, bool] = {}  # device index -> is gfx950 (device properties do not change)
+
+
+def _device_index(device: torch.device | str | int | None) -> int:
+    if device is None:
+        return torch.cuda.current_device()
+    if isinstance(device, int):
+        return device
+    device = torch.device(device)
+    return device.index if device.index is not None else torch.cuda.current_device()
+
+
 def mi355x_available(device: torch.device | str | int | None = None) -> bool:
     """Whether a gfx950 GPU is visible to torch (the reference's sm89_available)."""
 
-    if not torch.cuda.is_available():
+    if not _ARCH_OK and not torch.cuda.is_available():
         return False
-    props = torch.cuda.get_device_properties(device if device is not None else torch.cuda.current_device())
-    return str(getattr(props, "gcnArchName", "")).split(":")[0] == "gfx950"
+    index = _device_index(device)
+    ok = _ARCH_OK.get(index)
+    if ok is None:
+        if not torch.cuda.is_available():
+            return False
+        props = torch.cuda.get_device_properties(index)
+        ok = _ARCH_OK[index] = str(getattr(props, "gcnArchName", "")).split(":")[0] == "gfx950"
+    return ok
 
 
 def _supports_call(input, weight, weight_scale_inv, block_size, activation_scale) -> bool:
@@ -134,11 +152,10 @@ class _Workspace:
     def __init__(self) -> None:
         self._buffers: dict[tuple[int, int], torch.Tensor] = {}
 
-    def get(self, device: torch.device, nbytes: int) -> torch.Tensor | None:
+    def get(self, device: torch.device, nbytes: int, stream: int | None = None) -> torch.Tensor | None:
         if nbytes == 0:
             return None
-        stream = torch.cuda.current_stream(device)
-        key = (device.index if device.index is not None else torch.cuda.current_device(), stream.cuda_stream)
+        key = (_device_index(device), _stream_ptr(device) if stream is None else stream)
         buf = self._buffers.get(key)
         if buf is None or buf.numel() < nbytes:
             grown = max(nbytes, 0 if buf is None else 2 * buf.numel())
@@ -153,7 +170,14 @@ class _Workspace:
 _workspace = _Workspace()
 
 
+# torch's current HIP stream of a device as a raw handle; the private getter skips building a
+# Stream object (a few microseconds per call on the eager path).
+_current_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def _stream_ptr(device: torch.device) -> int:
+    if _current_raw_stream is not None:
+        return _current_raw_stream(_device_index(device))
     return torch.cuda.current_stream(device).cuda_stream
 
 
@@ -211,14 +235,14 @@ def launch_block_gemm(activation: torch.Tensor, weight: torch.Tensor, output: to
     lib = _lib.load()
     code = _config_code(config)
     nbytes = lib.mi355x_fp8_block_gemm_workspace_bytes(m, n, k, code)
-    ws = _workspace.get(output.device, nbytes)
+    stream = _stream_ptr(output.device)
+    ws = _workspace.get(output.device, nbytes, stream)
     _lib.check(lib.mi355x_fp8_block_gemm(
         activation.data_ptr(), activation.stride(0), activation_scales.data_ptr(),
         activation_scales.stride(0), activation_scales.stride(1), weight.data_ptr(), weight.stride(0),
         weight_scales.data_ptr(), weight_scales.stride(0), weight_scales.stride(1), output.data_ptr(),
         _dtype_code(output.dtype), output.stride(0), m, n, k,
-        None if ws is None else ws.data_ptr(), 0 if ws is None else ws.numel(), code,
-        _stream_ptr(output.device)))
+        None if ws is None else ws.data_ptr(), 0 if ws is None else ws.numel(), code, stream))
 
 
 def mi355x_fp8_linear(
@@ -272,12 +296,13 @@ def mi355x_fp8_linear(
     lib = _lib.load()
     code = _config_code(gemm_config)
     nbytes = lib.mi355x_fp8_linear_workspace_bytes(m, n, k, code)
-    ws = _workspace.get(input.device, nbytes)
+    stream = _stream_ptr(input.device)
+    ws = _workspace.get(input.device, nbytes, stream)
     _lib.check(lib.mi355x_fp8_linear(
         input_2d.data_ptr(), _dtype_code(input_2d.dtype), m, k, input_2d.stride(0), input_2d.stride(1),
         weight_2d.data_ptr(), weight_2d.stride(0), scales_2d.data_ptr(), scales_2d.stride(0),
         scales_2d.stride(1), n, output.data_ptr(), _dtype_code(out_dtype), output.stride(0),
-        ws.data_ptr(), ws.numel(), code, _stream_ptr(input.device)))
+        ws.data_ptr(), ws.numel(), code, stream))
     result = output.reshape(*input.shape[:-1], n)
     return result if bias is None else result + bias
 
