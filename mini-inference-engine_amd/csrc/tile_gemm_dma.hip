@@ -84,11 +84,13 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
 // a 32-bit per-lane offset, so the K loop spends no VALU on addresses.
 __device__ __forceinline__ void dma16(const void* base, uint32_t off, void* lds_dst) {
   asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base),
-               "s"(lds_addr(lds_dst)));
+               "s"(lds_addr(lds_dst))
+               : "memory");
 }
 __device__ __forceinline__ void dma4(const void* base, uint32_t off, void* lds_dst) {
   asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1" ::"v"(off), "s"(base),
-               "s"(lds_addr(lds_dst)));
+               "s"(lds_addr(lds_dst))
+               : "memory");
 }
 
 // s_waitcnt with vmcnt = N (6 bits: 3:0 and 15:14) and lgkmcnt = 0, expcnt left at its maximum.

@@ -221,17 +221,49 @@ def _config_code(config: FP8GemmConfig | None) -> int:
     return _lib.CONFIG_AUTO if config is None else config.kernel
 
 
+def _check_gemm_operands(activation: torch.Tensor, weight: torch.Tensor, output: torch.Tensor,
+                         activation_scales: torch.Tensor, weight_scales: torch.Tensor) -> None:
+    """Every shape, dtype, stride and device fact the C-ABI's kernels rely on but cannot
+    see (it receives bare pointers); a violation raises ValueError before any launch."""
+
+    tensors = (activation, weight, output, activation_scales, weight_scales)
+    if any(t.ndim != 2 for t in tensors):
+        raise ValueError("GEMM operands must be 2-D")
+    if activation.dtype != torch.float8_e4m3fn or weight.dtype != torch.float8_e4m3fn:
+        raise ValueError("activation and weight must be float8_e4m3fn")
+    if activation_scales.dtype != torch.float32 or weight_scales.dtype != torch.float32:
+        raise ValueError("activation and weight scales must be float32")
+    if output.dtype not in {torch.bfloat16, torch.float16}:
+        raise ValueError("output must be bfloat16 or float16")
+    m, k = activation.shape
+    n = weight.shape[0]
+    kb, nb = (k + 127) // 128, (n + 127) // 128
+    if weight.shape[1] != k:
+        raise ValueError(f"weight K {weight.shape[1]} != activation K {k}")
+    if tuple(output.shape) != (m, n):
+        raise ValueError(f"output shape {tuple(output.shape)} != ({m}, {n})")
+    if tuple(weight_scales.shape) != (nb, kb):
+        raise ValueError(f"weight scales shape {tuple(weight_scales.shape)} != ({nb}, {kb})")
+    if tuple(activation_scales.shape) != (m, kb):
+        raise ValueError(f"activation scales shape {tuple(activation_scales.shape)} != ({m}, {kb})")
+    for name, t in (("activation", activation), ("weight", weight), ("output", output)):
+        if t.stride(-1) != 1 or (t.shape[0] > 1 and t.stride(0) < t.shape[1]):
+            raise ValueError(f"{name} needs unit column stride and non-overlapping rows")
+    if any(st < 0 for t in (activation_scales, weight_scales) for st in t.stride()):
+        raise ValueError("scale strides must be nonnegative")
+    if len({t.device for t in tensors}) != 1 or not activation.is_cuda:
+        raise ValueError("GEMM operands must be on one GPU")
+
+
 def launch_block_gemm(activation: torch.Tensor, weight: torch.Tensor, output: torch.Tensor,
                       activation_scales: torch.Tensor, weight_scales: torch.Tensor,
                       config: FP8GemmConfig | None = None) -> None:
     """GEMM on pre-quantized activations into ``output`` (the reference's
     _launch_split_gemm, sm89_fp8.py:427-441).  ``config`` forces a kernel."""
 
+    _check_gemm_operands(activation, weight, output, activation_scales, weight_scales)
     m, k = activation.shape
     n = weight.shape[0]
-    for t in (activation, weight, output):
-        if t.stride(-1) != 1:
-            raise ValueError("activation, weight and output need unit column stride")
     lib = _lib.load()
     code = _config_code(config)
     nbytes = lib.mi355x_fp8_block_gemm_workspace_bytes(m, n, k, code)
@@ -311,41 +343,54 @@ def mi355x_fp8_linear(
 fp8_linear = mi355x_fp8_linear
 
 
-def pretune_mi355x_fp8(model: Any, max_tokens: int = MAX_M_BUCKET) -> int:
-    """Warm every (shape, row bucket) pair of a model's FP8 linears (sm89_fp8.py:531-558).
+def _fp8_linear_shapes(model: Any) -> list[tuple[torch.Tensor, torch.Tensor, tuple[int, ...]]]:
+    """``(weight, scales, block_size)`` of every module holding an e4m3fn weight with fp32 scales."""
 
-    There is no autotuner to run: kernel choice is a closed-form function of the shape.
-    Warming sizes each stream's workspace for the largest bucket so that later calls
-    (including ones under HIP-graph capture) allocate nothing.  Returns the number of
-    shape/bucket pairs.
+    found = []
+    for module in model.modules():
+        weight = getattr(module, "weight", None)
+        scales = getattr(module, "weight_scale_inv", None)
+        if isinstance(weight, torch.Tensor) and weight.dtype == torch.float8_e4m3fn and isinstance(scales, torch.Tensor):
+            found.append((weight, scales, tuple(getattr(module, "block_size", SUPPORTED_BLOCK_SIZE))))
+    return found
+
+
+def pretune_mi355x_fp8(model: Any, max_tokens: int = MAX_M_BUCKET) -> int:
+    """Make every later FP8 linear call of ``model`` allocation-free (the role of the
+    reference's pretune, sm89_fp8.py:531-558, which fills Triton's autotune cache).
+
+    Nothing here is tuned: the kernel is a closed-form choice from (M, N, K).  What a
+    call can still need is its workspace (the quantized activations and their scales),
+    so this reserves the current stream's workspace once, at the size the largest
+    shape needs at the ceiling bucket, and then runs each distinct (N, K) shape once
+    per row bucket so that every kernel the dispatch can pick is loaded before a HIP
+    graph is captured.  Returns the number of (shape, bucket) pairs warmed.
     """
 
-    shapes = {
-        (module.weight, module.weight_scale_inv, tuple(getattr(module, "block_size", SUPPORTED_BLOCK_SIZE)))
-        for module in model.modules()
-        if getattr(getattr(module, "weight", None), "dtype", None) == torch.float8_e4m3fn
-        and isinstance(getattr(module, "weight_scale_inv", None), torch.Tensor)
-    }
     dtype = next(p.dtype for p in model.parameters() if p.dtype in {torch.bfloat16, torch.float16})
-    return pretune_mi355x_fp8_shapes(shapes, dtype, max_tokens)
+    return pretune_mi355x_fp8_shapes(_fp8_linear_shapes(model), dtype, max_tokens)
 
 
 def pretune_mi355x_fp8_shapes(shapes: Any, dtype: torch.dtype, max_tokens: int = MAX_M_BUCKET) -> int:
     """``pretune_mi355x_fp8`` for explicit ``(weight, scales, block_size)`` triples."""
 
-    unique = {}
+    by_shape: dict[tuple[int, int], tuple[torch.Tensor, torch.Tensor, tuple[int, ...]]] = {}
     for weight, scales, block in shapes:
-        unique.setdefault(tuple(weight.shape), (weight, scales, tuple(block)))
+        by_shape.setdefault((int(weight.shape[0]), int(weight.shape[1])), (weight, scales, tuple(block)))
+    if not by_shape:
+        return 0
     buckets = pretune_row_buckets(int(max_tokens))
+    device = next(iter(by_shape.values()))[0].device
+    lib = _lib.load()
+    need = max(lib.mi355x_fp8_linear_workspace_bytes(buckets[-1], n, k, _lib.CONFIG_AUTO) for n, k in by_shape)
+    _workspace.get(device, need)
     with torch.inference_mode():
-        for weight, scales, block in unique.values():
+        for weight, scales, block in by_shape.values():
+            activation = torch.zeros((buckets[-1], weight.shape[1]), dtype=dtype, device=weight.device)
             for bucket in buckets:
-                activation = torch.zeros((bucket, weight.shape[1]), dtype=dtype, device=weight.device)
-                for rows in (bucket, bucket - 1) if bucket >= 16 else (bucket,):
-                    for path in ("fused", "split"):
-                        mi355x_fp8_linear(activation[:rows], weight, scales, block_size=list(block), path=path)
+                mi355x_fp8_linear(activation[:bucket], weight, scales, block_size=list(block))
     torch.cuda.synchronize()
-    return len(unique) * len(buckets)
+    return len(by_shape) * len(buckets)
 
 
 def install_mi355x_fp8_dispatch() -> dict[str, Any]:

@@ -7,6 +7,7 @@ from dataclasses import FrozenInstanceError
 import pytest
 import torch
 
+from minillm_amd import _lib
 from minillm_amd import mi355x_fp8 as fp8
 from minillm_amd.validation import (
     EXACT_MS, MODEL_SHAPES, QWEN3_4B_PROJECTIONS, bit_mismatch_details, bitwise_equal, gemm_bytes,
@@ -63,17 +64,18 @@ def fp8_model():
 
 
 @pytest.mark.parametrize("max_tokens", [1, 3, 17, 1000])
-def test_pretune_warms_both_specializations_and_deduplicates_shapes(monkeypatch, fp8_model, max_tokens):
-    calls = []
-    monkeypatch.setattr(fp8, "mi355x_fp8_linear", lambda x, w, s, **kw: calls.append((x.shape[0], kw["path"])))
+def test_pretune_reserves_workspace_once_and_warms_each_bucket_once(monkeypatch, fp8_model, max_tokens):
+    calls, reserved = [], []
+    monkeypatch.setattr(fp8, "mi355x_fp8_linear", lambda x, w, s, **kw: calls.append((x.shape[0], tuple(w.shape))))
+    monkeypatch.setattr(fp8._workspace, "get", lambda device, nbytes, stream=None: reserved.append(nbytes))
     monkeypatch.setattr(torch.cuda, "synchronize", lambda: None)
     buckets = fp8.pretune_row_buckets(max_tokens)
+    # Two modules share one (N, K): it is warmed once per bucket.
     assert fp8.pretune_mi355x_fp8(fp8_model, max_tokens=max_tokens) == len(buckets)
-    for bucket in buckets:
-        for path in ("fused", "split"):
-            rows = [m for m, p in calls if p == path and fp8.m_bucket(m) == bucket]
-            assert rows[0] == bucket
-            assert len(rows) == (2 if bucket >= 16 else 1)
+    assert calls == [(b, (129, 259)) for b in buckets]
+    lib = _lib.load()
+    assert reserved == [lib.mi355x_fp8_linear_workspace_bytes(buckets[-1], 129, 259, _lib.CONFIG_AUTO)]
+    assert reserved[0] >= lib.mi355x_fp8_linear_workspace_bytes(max(1, max_tokens), 129, 259, _lib.CONFIG_AUTO)
 
 
 def test_unsupported_calls_raise_without_fallback():
@@ -156,3 +158,31 @@ def test_roofline_byte_and_flop_counts():
     assert gemm_bytes(8, 6144, 2560) == 6144 * 2560 + 4 * 48 * 20 + 2 * 8 * 2560 + 2 * 8 * 6144
     assert quant_bytes(8, 2560) == 3 * 8 * 2560 + 4 * 8 * 20
     assert sum(p.n * p.k for p in QWEN3_4B_PROJECTIONS) == 100_925_440
+
+
+def _gemm_operands(m=5, n=130, k=260):
+    f8 = torch.float8_e4m3fn
+    return dict(activation=torch.zeros(m, k).to(f8), weight=torch.zeros(n, k).to(f8),
+                output=torch.empty(m, n, dtype=torch.bfloat16),
+                activation_scales=torch.ones(m, (k + 127) // 128), weight_scales=torch.ones((n + 127) // 128, (k + 127) // 128))
+
+
+@pytest.mark.parametrize("field,bad,match", [
+    ("output", torch.empty(4, 130, dtype=torch.bfloat16), "output shape"),
+    ("output", torch.empty(5, 130, dtype=torch.float32), "output must be"),
+    ("weight", torch.zeros(130, 259).to(torch.float8_e4m3fn), "weight K"),
+    ("weight_scales", torch.ones(1, 3), "weight scales shape"),
+    ("activation_scales", torch.ones(5, 2), "activation scales shape"),
+    ("activation_scales", torch.ones(4, 3), "activation scales shape"),
+    ("activation", torch.zeros(5, 260, dtype=torch.bfloat16), "e4m3fn"),
+    ("weight_scales", torch.ones(2, 3, dtype=torch.float64), "float32"),
+])
+def test_launch_block_gemm_rejects_mismatched_operands(field, bad, match):
+    """The C-ABI sees bare pointers: the Python entry checks every shape first."""
+
+    ops = _gemm_operands()
+    ops[field] = bad
+    with pytest.raises(ValueError, match=match):
+        fp8.launch_block_gemm(**ops)
+    with pytest.raises(ValueError, match="one GPU"):  # well-formed, but on the CPU
+        fp8.launch_block_gemm(**_gemm_operands())
