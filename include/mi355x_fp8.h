@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define MI355X_FP8_ABI_VERSION 1
+#define MI355X_FP8_ABI_VERSION 2
 
 /* Element types of activations and outputs. */
 #define MI355X_FP8_DTYPE_BF16 0
@@ -41,6 +41,11 @@ extern "C" {
 #define MI355X_FP8_ERR_UNSUPPORTED 2 /* valid but not supported here (RuntimeError) */
 #define MI355X_FP8_ERR_WORKSPACE 3   /* workspace missing or too small (ValueError) */
 #define MI355X_FP8_ERR_LAUNCH 4      /* HIP launch failure (RuntimeError) */
+#define MI355X_FP8_ERR_SCRATCH 5     /* larger than the static scratch of the no-allocation
+                                        entry point (ValueError) */
+
+/* Bytes of device scratch each GPU holds for mi355x_fp8_linear_noalloc (24 MiB). */
+#define MI355X_FP8_NOALLOC_SCRATCH_BYTES (24u << 20)
 
 /* Version of this ABI; equals MI355X_FP8_ABI_VERSION of the header it was built with. */
 int mi355x_fp8_abi_version(void);
@@ -97,6 +102,24 @@ int mi355x_fp8_linear(const void* x, int x_dtype, int64_t M, int64_t K, int64_t 
                       int64_t ws_sn, int64_t ws_sk, int64_t N, void* out, int out_dtype,
                       int64_t ldo, void* workspace, size_t workspace_bytes, int config,
                       void* stream);
+
+/*
+ * mi355x_fp8_linear without a workspace argument: no reference counterpart.  For callers
+ * that cannot allocate device memory (code under HIP-graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  The quantized activations and their scales go to a
+ * static device array of MI355X_FP8_NOALLOC_SCRATCH_BYTES per GPU (held until the process
+ * ends); calls whose mi355x_fp8_linear_workspace_bytes exceed it return
+ * MI355X_FP8_ERR_SCRATCH before launching anything.  The call allocates nothing and gives
+ * the bits of mi355x_fp8_linear.  Every call on one GPU shares that GPU's scratch:
+ * calls that overlap in time on one GPU (different streams, or host threads) race.
+ */
+int mi355x_fp8_linear_noalloc(const void* x, int x_dtype, int64_t M, int64_t K, int64_t sxm,
+                              int64_t sxk, const uint8_t* w, int64_t ldw, const float* ws,
+                              int64_t ws_sn, int64_t ws_sk, int64_t N, void* out, int out_dtype,
+                              int64_t ldo, int config, void* stream);
+
+/* MI355X_FP8_NOALLOC_SCRATCH_BYTES, as built into the library. */
+size_t mi355x_fp8_linear_noalloc_scratch_bytes(void);
 
 /*
  * Fused SiLU(gate) * up followed by the activation quantizer, for the MLP's down_proj.

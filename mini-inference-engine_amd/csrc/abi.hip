@@ -2,7 +2,16 @@
 // Argument validation lives here; the kernels assume validated shapes.
 #include "fp8_abi_internal.h"
 
+#include <mutex>
+
 using namespace mi355x;
+
+// Device-resident scratch of mi355x_fp8_linear_noalloc: the quantized activations and their
+// scales.  Every GPU the library runs on holds its own copy until the process ends.  Host
+// code must never pass this name to a kernel (on the host it is only a stand-in for the
+// symbol): the device address comes from hipGetSymbolAddress, per device, in
+// scratch_ptr().
+static __device__ __align__(256) uint8_t scratch[MI355X_FP8_NOALLOC_SCRATCH_BYTES];
 
 namespace {
 
@@ -30,6 +39,24 @@ int linear_layout(int64_t M, int64_t N, int64_t K, int config, LinearLayout* L) 
   return MI355X_FP8_OK;
 }
 
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// The current device's address of `scratch`, looked up once per device (with that device
+// current, as hipGetSymbolAddress answers for the current device).  nullptr on failure.
+void* scratch_ptr() {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* ptr = nullptr;
+    if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || ptr == nullptr) return nullptr;
+    g_scratch_ptr[dev] = ptr;
+  }
+  return g_scratch_ptr[dev];
+}
+
 }  // namespace
 
 extern "C" {
@@ -43,6 +70,7 @@ const char* mi355x_fp8_status_string(int status) {
     case MI355X_FP8_ERR_UNSUPPORTED: return "unsupported call";
     case MI355X_FP8_ERR_WORKSPACE: return "workspace missing or too small";
     case MI355X_FP8_ERR_LAUNCH: return "HIP kernel launch failed";
+    case MI355X_FP8_ERR_SCRATCH: return "call needs more than the library's static scratch";
     default: return "unknown status";
   }
 }
@@ -142,6 +170,28 @@ int mi355x_fp8_linear(const void* x, int x_dtype, int64_t M, int64_t K, int64_t 
   if (st != MI355X_FP8_OK) return st;
   return launch_block_gemm(L.plan, q, L.kpad, as, 1, L.mpad, w, ldw, ws, ws_sn, ws_sk, out, out_dtype,
                            ldo, M, N, K, workspace, s);
+}
+
+size_t mi355x_fp8_linear_noalloc_scratch_bytes(void) { return MI355X_FP8_NOALLOC_SCRATCH_BYTES; }
+
+int mi355x_fp8_linear_noalloc(const void* x, int x_dtype, int64_t M, int64_t K, int64_t sxm, int64_t sxk,
+                              const uint8_t* w, int64_t ldw, const float* ws, int64_t ws_sn, int64_t ws_sk,
+                              int64_t N, void* out, int out_dtype, int64_t ldo, int config, void* stream) {
+  if (!valid_dtype(x_dtype) || !valid_dtype(out_dtype) || M < 0 || N < 0 || K <= 0 || ldw < K || ldo < N)
+    return MI355X_FP8_ERR_INVALID;
+  LinearLayout L;
+  int st = linear_layout(M, N, K, config, &L);
+  if (st != MI355X_FP8_OK) return st;
+  if (M == 0 || N == 0) return MI355X_FP8_OK;
+  if (!x || !w || !ws || !out) return MI355X_FP8_ERR_INVALID;
+  if (L.total > MI355X_FP8_NOALLOC_SCRATCH_BYTES) return MI355X_FP8_ERR_SCRATCH;
+  void* base = scratch_ptr();
+  if (base == nullptr) return MI355X_FP8_ERR_LAUNCH;
+  // Same kernels and layout as mi355x_fp8_linear, with the scratch in place of the caller's
+  // workspace.  Every byte the GEMM reads is written by the quantizer first in stream order
+  // (codes up to Kpad, scales of rows < M), so nothing needs clearing between calls.
+  return mi355x_fp8_linear(x, x_dtype, M, K, sxm, sxk, w, ldw, ws, ws_sn, ws_sk, N, out, out_dtype, ldo, base,
+                           L.total, config, stream);
 }
 
 }  // extern "C"

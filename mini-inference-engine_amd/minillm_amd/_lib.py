@@ -20,7 +20,7 @@ _ptr = ctypes.c_void_p
 _size = ctypes.c_size_t
 
 # Mirrors include/mi355x_fp8.h.
-ABI_VERSION = 1
+ABI_VERSION = 2
 DTYPE_BF16 = 0
 DTYPE_F16 = 1
 CONFIG_AUTO = 0
@@ -32,6 +32,8 @@ ERR_INVALID = 1
 ERR_UNSUPPORTED = 2
 ERR_WORKSPACE = 3
 ERR_LAUNCH = 4
+ERR_SCRATCH = 5
+NOALLOC_SCRATCH_BYTES = 24 << 20
 
 EXPORTS = {
     "mi355x_fp8_abi_version": ([], _int),
@@ -45,6 +47,9 @@ EXPORTS = {
     "mi355x_fp8_rmsnorm_quant": ([_ptr, _int, _i64, _i64, _i64, _ptr, _i64, _ptr, _i64, _ptr, ctypes.c_float, _ptr,
                                   _i64, _ptr, _i64, _i64, _ptr, _i64, _i64, _ptr], _int),
     "mi355x_fp8_linear_workspace_bytes": ([_i64, _i64, _i64, _int], _size),
+    "mi355x_fp8_linear_noalloc": ([_ptr, _int, _i64, _i64, _i64, _i64, _ptr, _i64, _ptr, _i64, _i64, _i64, _ptr,
+                                   _int, _i64, _int, _ptr], _int),
+    "mi355x_fp8_linear_noalloc_scratch_bytes": ([], _size),
     "mi355x_fp8_linear": ([_ptr, _int, _i64, _i64, _i64, _i64, _ptr, _i64, _ptr, _i64, _i64, _i64, _ptr, _int,
                            _i64, _ptr, _size, _int, _ptr], _int),
 }
@@ -78,6 +83,6 @@ def check(status: int) -> None:
     if status == OK:
         return
     text = load().mi355x_fp8_status_string(status).decode()
-    if status in (ERR_INVALID, ERR_WORKSPACE):
+    if status in (ERR_INVALID, ERR_WORKSPACE, ERR_SCRATCH):
         raise ValueError(f"libmi355x_fp8: {text}")
     raise RuntimeError(f"libmi355x_fp8: {text} (status {status})")

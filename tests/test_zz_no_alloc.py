@@ -1,0 +1,68 @@
+"""The no-allocation entry point mi355x_fp8_linear_noalloc, through the C-ABI.
+
+It must give the bits of mi355x_fp8_linear (the workspace entry point) on the same inputs,
+on two calls in a row (the second smaller, so stale scratch contents from the first call
+would show), allocate no torch memory, and reject a call larger than its static scratch
+before launching anything.
+"""
+
+import sys
+
+import pytest
+import torch
+
+from minillm_amd import _lib
+from minillm_amd import mi355x_fp8 as fp8
+from minillm_amd.validation import ModelShape, bit_mismatch_details, bitwise_equal, make_activations, make_weights
+
+pytestmark = pytest.mark.gpu
+
+
+def _noalloc(x, w, ws, out, config=_lib.CONFIG_AUTO):
+    m, k = x.shape
+    stream = torch.cuda.current_stream(x.device).cuda_stream
+    return _lib.load().mi355x_fp8_linear_noalloc(
+        x.data_ptr(), _lib.DTYPE_BF16 if x.dtype == torch.bfloat16 else _lib.DTYPE_F16, m, k, x.stride(0),
+        x.stride(1), w.data_ptr(), w.stride(0), ws.data_ptr(), ws.stride(0), ws.stride(1), w.shape[0],
+        out.data_ptr(), _lib.DTYPE_BF16 if out.dtype == torch.bfloat16 else _lib.DTYPE_F16, out.stride(0), config,
+        stream)
+
+
+@pytest.mark.parametrize("first,second", [((2048, 2560, 9728), (8, 2560, 9728)),
+                                          ((536, 19456, 2560), (16, 6144, 2560)),
+                                          ((300, 193, 259), (7, 129, 127))])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_noalloc_equals_workspace_entry_twice(gpu, first, second, dtype):
+    print("CASE noalloc", first, second, dtype, flush=True, file=sys.stderr)
+    lib = _lib.load()
+    assert lib.mi355x_fp8_linear_noalloc_scratch_bytes() == _lib.NOALLOC_SCRATCH_BYTES
+    cases = []
+    for i, (m, n, k) in enumerate((first, second)):
+        x = make_activations(m, k, 30 + i, dtype).to(gpu)
+        w, ws = make_weights(ModelShape("noalloc", n, k), 30 + i)
+        cases.append((x, w.to(gpu), ws.to(gpu)))
+    outs = [torch.full((x.shape[0], w.shape[0]), float("nan"), dtype=dtype, device=gpu) for x, w, _ in cases]
+    torch.cuda.synchronize()
+    before = torch.cuda.memory_allocated(gpu)
+    for (x, w, ws), out in zip(cases, outs):
+        _lib.check(_noalloc(x, w, ws, out))
+    torch.cuda.synchronize()
+    assert torch.cuda.memory_allocated(gpu) == before
+    for (x, w, ws), out in zip(cases, outs):
+        ref = fp8.mi355x_fp8_linear(x, w, ws, [128, 128])
+        assert bitwise_equal(out, ref), bit_mismatch_details(out, ref)
+
+
+def test_noalloc_rejects_calls_beyond_the_scratch(gpu):
+    lib = _lib.load()
+    m, k, n = 4096, 9728, 256  # q alone is 39.8 MB > 24 MiB
+    assert lib.mi355x_fp8_linear_workspace_bytes(m, n, k, 0) > _lib.NOALLOC_SCRATCH_BYTES
+    x = torch.zeros((m, k), dtype=torch.bfloat16, device=gpu)
+    w = torch.zeros((n, k), dtype=torch.uint8, device=gpu).view(torch.float8_e4m3fn)
+    ws = torch.ones((2, 76), dtype=torch.float32, device=gpu)
+    out = torch.full((m, n), 7.0, dtype=torch.bfloat16, device=gpu)
+    assert _noalloc(x, w, ws, out) == _lib.ERR_SCRATCH
+    with pytest.raises(ValueError, match="scratch"):
+        _lib.check(_lib.ERR_SCRATCH)
+    torch.cuda.synchronize()
+    assert (out == 7.0).all().item()  # nothing was launched
