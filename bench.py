@@ -140,8 +140,11 @@ def main(argv=None) -> int:
     print(f"generating {sets} weight sets of {layer_bytes / 2**20:.1f} MiB", file=sys.stderr, flush=True)
     weights = [[make_baseline_weights(p, SEED + 1000 * s, device="cuda") for p in projs] for s in range(sets)]
 
-    def run_phase(m, outliers, full_linear):
-        per_launch, quant, linear = [], [], []
+    lib = fp8._lib.load()
+    sink = torch.empty(8 * 1024, dtype=torch.int32, device=dev)
+
+    def run_phase(m, outliers, full_linear, probe=False):
+        per_launch, quant, linear, probes = [], [], [], []
         for i, p in enumerate(projs):
             x = make_baseline_activations(m, p.k, SEED, outliers=outliers, device="cuda")
             q, s = fp8.quantize_mi355x_fp8_activation(x, scale_layout="kgroup")
@@ -159,18 +162,26 @@ def main(argv=None) -> int:
                 for r in range(sets):
                     fp8.mi355x_fp8_linear(x, weights[r][i][0], weights[r][i][1], [128, 128])
 
+            def reads(i=i):
+                for r in range(sets):
+                    w8 = weights[r][i][0]
+                    fp8._lib.check(lib.mi355x_fp8_read_probe(w8.data_ptr(), w8.numel(), sink.data_ptr(), sink.numel(),
+                                                             torch.cuda.current_stream().cuda_stream))
+
             per_launch.append(timed_graph(torch, stream, gemms, sets, args.steps, args.warmup, args.eager))
+            if probe:
+                probes.append(timed_graph(torch, stream, reads, sets, args.steps, args.warmup, args.eager))
             quant.append(timed_graph(torch, stream, quants, sets, args.steps, args.warmup, args.eager))
             if full_linear:
                 linear.append(timed_graph(torch, stream, linears, sets, args.steps, args.warmup, args.eager))
-        return per_launch, quant, linear
+        return per_launch, quant, linear, probes
 
     results = {}
     for phase, m, outliers in (("prefill", args.prefill_m, True), ("decode", args.decode_m, False)):
         if args.only and phase != args.only:
             continue
         print(f"timing {phase} M={m}", file=sys.stderr, flush=True)
-        mean, quant_ms, linear_ms = run_phase(m, outliers, full_linear=phase == "decode")
+        mean, quant_ms, linear_ms, probe_ms = run_phase(m, outliers, full_linear=True, probe=phase == "decode")
         flops = [linear_flops(m, p.n, p.k) for p in projs]
         nbytes = [gemm_bytes(m, p.n, p.k) for p in projs]
         results[phase] = {
@@ -185,17 +196,27 @@ def main(argv=None) -> int:
             "quant": {p.name: {"us": 1e3 * quant_ms[i], "gbps": quant_bytes(m, p.k) / (quant_ms[i] * 1e6)}
                       for i, p in enumerate(projs)},
         }
+        if probe_ms:
+            # The same launches, each a plain streaming read of its weight bytes: what one launch
+            # over these bytes reaches (launch, ramp-up and drain included).
+            results[phase]["read_ceiling"] = {
+                "step_ms": sum(probe_ms), "gbps": sum(nbytes) / (sum(probe_ms) * 1e6),
+                "per_proj_us": {p.name: 1e3 * probe_ms[i] for i, p in enumerate(projs)}}
         if linear_ms:
             # The whole linear from bf16 activations (quantization included), as a model calls
             # it; same algorithmic bytes (gemm_bytes counts the activations as bf16).
             lbytes = nbytes
             results[phase]["linear"] = {
                 "step_ms": sum(linear_ms), "gbps": sum(lbytes) / (sum(linear_ms) * 1e6),
+                "tflops": sum(flops) / (sum(linear_ms) * 1e9),
                 "per_proj": {p.name: {"us": 1e3 * linear_ms[i], "gbps": lbytes[i] / (linear_ms[i] * 1e6)}
                              for i, p in enumerate(projs)}}
     if args.only:
         print(json.dumps({"phase": args.only, "detail": results}), flush=True)
         return 0
+    if "decode" in results:
+        print("timing the decode layer chain", file=sys.stderr, flush=True)
+        results["decode"]["layer_chain"] = bench_decode_layers(torch, fp8, stream, args, weights, projs)
     del weights
     torch.cuda.empty_cache()
 
@@ -235,19 +256,58 @@ def main(argv=None) -> int:
         "decode": {"gbps": round(dec["gbps"], 1), "ms_per_step": round(dec["step_ms"], 4),
                    "frac_of_hbm": round(dec["gbps"] / PEAK_HBM_GBPS, 4),
                    "linear_gbps": round(dec["linear"]["gbps"], 1),
-                   "linear_ms_per_step": round(dec["linear"]["step_ms"], 4)},
+                   "linear_ms_per_step": round(dec["linear"]["step_ms"], 4),
+                   "layer_chain_gbps": dec["layer_chain"]["weight_gbps"],
+                   "layer_chain_us_per_layer": dec["layer_chain"]["us_per_layer"]},
+        "prefill_linear": {"tflops": round(pre["linear"]["tflops"], 1), "ms_per_step": round(pre["linear"]["step_ms"], 4),
+                           "frac": round(pre["linear"]["tflops"] / PEAK_FP8_TFLOPS, 4)},
         "roofline": {"bound": "mfma", "kernel": "prefill block GEMM (M=2048, mean over the 4 projections)",
                      "achieved": round(pre["tflops"], 2), "peak": PEAK_FP8_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(pre["tflops"] / PEAK_FP8_TFLOPS, 4), "traffic": traffic_per_launch("prefill")},
         "roofline_decode": {"bound": "hbm", "kernel": "stream_gemm_kernel (decode M=8, mean over the 4 projections)",
                             "achieved": round(dec["gbps"], 1), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
-                            "frac": round(dec["gbps"] / PEAK_HBM_GBPS, 4), "traffic": traffic_per_launch("decode")},
+                            "frac": round(dec["gbps"] / PEAK_HBM_GBPS, 4), "traffic": traffic_per_launch("decode"),
+                            "ceiling": round(dec["read_ceiling"]["gbps"], 1),
+                            "frac_of_ceiling": round(dec["gbps"] / dec["read_ceiling"]["gbps"], 4)},
         "extras": extras,
         "detail": results,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
     return 0
+
+
+def bench_decode_layers(torch, fp8, stream, args, weights, projs):
+    """The decode linears as a model runs them, chained over the rotating weight sets (one
+    set per layer): residual add + RMSNorm + quantizer -> qkv GEMM; the q columns (the
+    attention stand-in) -> quantizer + o_proj GEMM; residual add + RMSNorm + quantizer ->
+    gate_up GEMM; SiLU*up + quantizer -> down GEMM.  Eight launches per layer, none of them a
+    standalone quantizer in front of qkv, gate_up or down.  Reported: time per layer and the
+    layer's weight bytes per second."""
+
+    m, hidden, eps = args.decode_m, 2560, 1e-6
+    gen = torch.Generator().manual_seed(SEED + 3)
+    h0 = torch.randn(m, hidden, generator=gen).to(torch.bfloat16).cuda()
+    r0 = torch.randn(m, hidden, generator=gen).to(torch.bfloat16).cuda()
+    norms = [((torch.rand(hidden, generator=gen) + 0.5).to(torch.bfloat16).cuda(),
+              (torch.rand(hidden, generator=gen) + 0.5).to(torch.bfloat16).cuda()) for _ in weights]
+    inter = projs[3].k
+    out = torch.empty((m, hidden), dtype=torch.bfloat16, device="cuda")
+
+    def chain():
+        h, res = h0, r0
+        for (qkv_w, o_w, gu_w, d_w), (n1, n2) in zip(weights, norms):
+            qkv, summed = fp8.rmsnorm_linear_mi355x_fp8(h, n1, eps, qkv_w[0], qkv_w[1], residual=res)
+            o = fp8.mi355x_fp8_linear(qkv[:, :projs[1].k], o_w[0], o_w[1], [128, 128])
+            gu, res = fp8.rmsnorm_linear_mi355x_fp8(o, n2, eps, gu_w[0], gu_w[1], residual=summed)
+            q3, s3 = fp8.silu_mul_quant_mi355x_fp8(gu[:, :inter], gu[:, inter:])
+            fp8.launch_block_gemm(q3, d_w[0], out, s3, d_w[1])
+            h = out
+
+    ms = timed_graph(torch, stream, chain, len(weights), args.steps, args.warmup, args.eager)
+    nbytes = sum(p.n * p.k + 4 * ((p.n + 127) // 128) * ((p.k + 127) // 128) for p in projs)
+    return {"us_per_layer": round(ms * 1e3, 2), "weight_gbps": round(nbytes / (ms * 1e6), 1),
+            "launches_per_layer": 8}
 
 
 def bench_rmsnorm_quant(torch, fp8, stream, args):
@@ -326,7 +386,9 @@ def cpu_baseline(rows: int) -> dict:
     import oracle
     from minillm_amd.validation import QWEN3_4B_PROJECTIONS, make_baseline_activations, make_baseline_weights
 
-    threads = min(os.cpu_count() or 1, 16)
+    host_cpus = os.cpu_count() or 1
+    # The GPU box's CPU share is 16 cores per GPU (the pool's rule), whatever the host shows.
+    threads = min(host_cpus, 16)
     total_flops, total_s = 0, 0.0
     for p in QWEN3_4B_PROJECTIONS:
         w, ws = make_baseline_weights(p, SEED)
@@ -338,7 +400,21 @@ def cpu_baseline(rows: int) -> dict:
         oracle.block_gemm(q, s, wc, wsn, threads=threads)
         total_s += time.perf_counter() - t0
         total_flops += 2 * rows * p.n * p.k
+    # Config 1 of the baseline as the reference's CPU path runs it: the merged qkv linear
+    # (quantizer + GEMM) on 16 tokens, single-threaded and with the same thread count.
+    qkv = QWEN3_4B_PROJECTIONS[0]
+    w, ws = make_baseline_weights(qkv, SEED)
+    x16 = make_baseline_activations(16, qkv.k, SEED).view(torch.int16).numpy().view(np.uint16)
+    wc, wsn = w.view(torch.uint8).numpy(), ws.numpy()
+    config1 = {}
+    for label, th in (("1_thread", 1), (f"{threads}_threads", threads)):
+        t0 = time.perf_counter()
+        reps = 3
+        for _ in range(reps):
+            oracle.linear(x16, wc, wsn, threads=th)
+        config1[label + "_ms"] = round((time.perf_counter() - t0) / reps * 1e3, 2)
     return {"value": round(total_flops / total_s / 1e12, 5), "unit": "TFLOPS", "cores": threads,
+            "host_cpus": host_cpus, "config1_qkv_m16": config1,
             "kind": "port",
             "sample": f"C oracle block GEMM (exact fp64 per-group dots, fp32 scaling) over the 4 projections "
                       f"at M={rows}, {total_s:.1f} s"}

@@ -122,6 +122,15 @@ int mi355x_fp8_linear_noalloc(const void* x, int x_dtype, int64_t M, int64_t K, 
 size_t mi355x_fp8_linear_noalloc_scratch_bytes(void);
 
 /*
+ * Measurement helper, no reference counterpart: reads `bytes` of device memory at `src`
+ * once (16-byte loads over all CUs) and nothing else, so that a benchmark can time the
+ * streaming-read rate one launch reaches over the same bytes as a decode GEMM.  bytes must
+ * be a multiple of 16 and src 16-byte aligned; sink is a device buffer of sink_words >=
+ * 8 x (number of CUs) 32-bit words (its contents are unspecified afterwards).
+ */
+int mi355x_fp8_read_probe(const void* src, size_t bytes, void* sink, size_t sink_words, void* stream);
+
+/*
  * Fused SiLU(gate) * up followed by the activation quantizer, for the MLP's down_proj.
  * Replaces silu_mul (engine/kernels/fused.py:127-137, 217-232) plus the quantizer launch of
  * the down projection (engine/kernels/sm89_fp8.py:401-424) in _mlp_forward

@@ -172,6 +172,10 @@ int mi355x_fp8_linear(const void* x, int x_dtype, int64_t M, int64_t K, int64_t 
                            ldo, M, N, K, workspace, s);
 }
 
+int mi355x_fp8_read_probe(const void* src, size_t bytes, void* sink, size_t sink_words, void* stream) {
+  return launch_read_probe(src, bytes, sink, sink_words, static_cast<hipStream_t>(stream));
+}
+
 size_t mi355x_fp8_linear_noalloc_scratch_bytes(void) { return MI355X_FP8_NOALLOC_SCRATCH_BYTES; }
 
 int mi355x_fp8_linear_noalloc(const void* x, int x_dtype, int64_t M, int64_t K, int64_t sxm, int64_t sxk,

@@ -59,6 +59,10 @@ int tile256_width(int64_t M, int64_t N, int64_t cus);
 // Whether the 256-row kernel's 32-bit byte offsets reach every byte of q and W.
 bool tile256_offsets_ok(int64_t ldq, int64_t ldw, int64_t M, int64_t N, int64_t K);
 
+// Streaming read of `bytes` (a multiple of 16, 16-byte aligned) for the decode ceiling;
+// sink holds sink_words >= 8 x CUs words.
+int launch_read_probe(const void* src, size_t bytes, void* sink, size_t sink_words, hipStream_t stream);
+
 // Compute units of the current device (cached per device; 256 if it cannot be queried).
 int64_t device_cus();
 

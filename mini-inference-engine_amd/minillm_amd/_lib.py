@@ -50,6 +50,7 @@ EXPORTS = {
     "mi355x_fp8_linear_noalloc": ([_ptr, _int, _i64, _i64, _i64, _i64, _ptr, _i64, _ptr, _i64, _i64, _i64, _ptr,
                                    _int, _i64, _int, _ptr], _int),
     "mi355x_fp8_linear_noalloc_scratch_bytes": ([], _size),
+    "mi355x_fp8_read_probe": ([_ptr, _size, _ptr, _size, _ptr], _int),
     "mi355x_fp8_linear": ([_ptr, _int, _i64, _i64, _i64, _i64, _ptr, _i64, _ptr, _i64, _i64, _i64, _ptr, _int,
                            _i64, _ptr, _size, _int, _ptr], _int),
 }

@@ -16,7 +16,7 @@ CSRC_DIR = os.path.join(os.path.dirname(PACKAGE_DIR), "csrc")
 LIB_DIR = os.path.join(PACKAGE_DIR, "lib")
 LIB_PATH = os.path.join(LIB_DIR, "libmi355x_fp8.so")
 SOURCES = ("act_quant.hip", "block_gemm.hip", "tile_gemm_dma.hip", "tile_gemm_256.hip", "silu_mul_quant.hip",
-           "rmsnorm_quant.hip", "abi.hip")
+           "rmsnorm_quant.hip", "read_probe.hip", "abi.hip")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 FLAGS = (

@@ -38,6 +38,7 @@ def test_header_constants_match_binding():
                          "MI355X_FP8_CONFIG_TILE256": _lib.CONFIG_TILE256, "MI355X_FP8_OK": _lib.OK,
                          "MI355X_FP8_ERR_INVALID": _lib.ERR_INVALID, "MI355X_FP8_ERR_UNSUPPORTED": _lib.ERR_UNSUPPORTED,
                          "MI355X_FP8_ERR_WORKSPACE": _lib.ERR_WORKSPACE, "MI355X_FP8_ERR_LAUNCH": _lib.ERR_LAUNCH,
+                         "MI355X_FP8_ERR_SCRATCH": _lib.ERR_SCRATCH,
                          "MI355X_FP8_ABI_VERSION": _lib.ABI_VERSION}.items():
         assert re.search(rf"#define {macro} {value}\b", text), macro
 
@@ -85,3 +86,11 @@ def test_argument_validation_happens_before_any_launch():
     dummy = ctypes.c_void_p(16)
     assert lib.mi355x_fp8_linear(dummy, 0, 4, 128, 128, 1, dummy, 128, dummy, 1, 1, 64, dummy, 0, 64, null, 0, 0,
                                  null) == _lib.ERR_WORKSPACE
+
+
+def test_read_probe_validates_on_the_host():
+    lib = _lib.load()
+    dummy = ctypes.c_void_p(16)
+    assert lib.mi355x_fp8_read_probe(None, 16, dummy, 4096, None) == _lib.ERR_INVALID
+    assert lib.mi355x_fp8_read_probe(dummy, 15, dummy, 4096, None) == _lib.ERR_INVALID   # not whole 16-byte units
+    assert lib.mi355x_fp8_read_probe(dummy, 0, dummy, 4096, None) == _lib.OK             # nothing to read
