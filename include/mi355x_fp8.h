@@ -32,8 +32,21 @@ extern "C" {
 #define MI355X_FP8_CONFIG_AUTO 0
 #define MI355X_FP8_CONFIG_STREAM 1  /* weight-streaming decode kernel (auto: up to 64 rows) */
 #define MI355X_FP8_CONFIG_TILE128 2 /* LDS-tiled 128x128 MFMA kernel, any M */
-#define MI355X_FP8_CONFIG_TILE256 3 /* 256x256 MFMA kernel; needs K % 128 == 0, 16-byte
-                                       aligned q/w and K-group-major activation scales */
+#define MI355X_FP8_CONFIG_TILE256 3 /* 256-row MFMA kernel, width by cost model; needs K % 128
+                                       == 0, 16-byte aligned q/w and K-group-major activation
+                                       scales */
+/* One prefill kernel variant each (same preconditions as TILE256; otherwise the call returns
+ * MI355X_FP8_ERR_UNSUPPORTED): the 128-row LDS-DMA kernel at width 64, 128 or 160, and the
+ * 256-row kernel at width 128, 160, 192, 224 or 256.  Every config gives the same bits; these
+ * exist for tuning and so that tests can reach each variant. */
+#define MI355X_FP8_CONFIG_DMA128_64 4
+#define MI355X_FP8_CONFIG_DMA128_128 5
+#define MI355X_FP8_CONFIG_DMA128_160 6
+#define MI355X_FP8_CONFIG_T256_128 7
+#define MI355X_FP8_CONFIG_T256_160 8
+#define MI355X_FP8_CONFIG_T256_192 9
+#define MI355X_FP8_CONFIG_T256_224 10
+#define MI355X_FP8_CONFIG_T256_256 11
 
 /* Status codes. */
 #define MI355X_FP8_OK 0

@@ -431,9 +431,7 @@ int plan_gemm(int64_t M, int64_t N, int64_t K, int config, GemmPlan* plan) {
                         (M <= 32 && cdiv(N, 16) <= 2 * device_cus());
     config = stream ? MI355X_FP8_CONFIG_STREAM : MI355X_FP8_CONFIG_TILE128;
   }
-  if (config != MI355X_FP8_CONFIG_STREAM && config != MI355X_FP8_CONFIG_TILE128 &&
-      config != MI355X_FP8_CONFIG_TILE256)
-    return MI355X_FP8_ERR_INVALID;
+  if (config < MI355X_FP8_CONFIG_STREAM || config > MI355X_FP8_CONFIG_T256_256) return MI355X_FP8_ERR_INVALID;
   plan->kernel = config;
   if (config != MI355X_FP8_CONFIG_STREAM) return MI355X_FP8_OK;
   // One 16-token tile per workgroup up to 16 rows, else slices of 32 rows (two tiles), one
@@ -602,6 +600,15 @@ int launch_block_gemm(const GemmPlan& plan, const uint8_t* q, int64_t ldq, const
                       int64_t M, int64_t N, int64_t K, void* workspace, hipStream_t stream) {
   if (M == 0 || N == 0) return MI355X_FP8_OK;
   const bool dma_ok = tile_dma_supported(q, ldq, as_sm, as_sk, w, ldw, M, K);
+  if (plan.kernel >= MI355X_FP8_CONFIG_DMA128_64) {
+    // A forced variant: the LDS-DMA preconditions, and for 256-row tiles their 32-bit offsets.
+    static constexpr int kWidth[] = {64, 128, 160, 128, 160, 192, 224, 256};
+    const int bn = kWidth[plan.kernel - MI355X_FP8_CONFIG_DMA128_64];
+    if (!dma_ok) return MI355X_FP8_ERR_UNSUPPORTED;
+    if (plan.kernel <= MI355X_FP8_CONFIG_DMA128_160)
+      return launch_tile_dma(q, ldq, as, as_sk, w, ldw, ws, ws_sn, ws_sk, out, out_dtype, ldo, M, N, K, bn, stream);
+    return launch_tile256(q, ldq, as, as_sk, w, ldw, ws, ws_sn, ws_sk, out, out_dtype, ldo, M, N, K, bn, stream);
+  }
   if (plan.kernel == MI355X_FP8_CONFIG_TILE256) {
     if (!dma_ok) return MI355X_FP8_ERR_UNSUPPORTED;
     return launch_tile256(q, ldq, as, as_sk, w, ldw, ws, ws_sn, ws_sk, out, out_dtype, ldo, M, N, K,

@@ -27,6 +27,8 @@ CONFIG_AUTO = 0
 CONFIG_STREAM = 1
 CONFIG_TILE128 = 2
 CONFIG_TILE256 = 3
+CONFIG_DMA128_64, CONFIG_DMA128_128, CONFIG_DMA128_160 = 4, 5, 6
+CONFIG_T256_128, CONFIG_T256_160, CONFIG_T256_192, CONFIG_T256_224, CONFIG_T256_256 = 7, 8, 9, 10, 11
 OK = 0
 ERR_INVALID = 1
 ERR_UNSUPPORTED = 2

@@ -52,11 +52,26 @@ class FP8GemmConfig:
     def label(self) -> str:
         return f"{self.name}:{self.block_m}x{self.block_n}x{self.block_k}"
 
+    @property
+    def needs_dma(self) -> bool:
+        """Runs only on LDS-DMA operands: K % 128 == 0, 16-byte aligned codes and
+        K-group-major activation scales (other calls raise "unsupported")."""
+        return self.kernel >= _lib.CONFIG_TILE256
+
 
 GEMM_CONFIGS = (
     FP8GemmConfig("stream", _lib.CONFIG_STREAM, 64, 64),
     FP8GemmConfig("tile128", _lib.CONFIG_TILE128, 128, 128),
     FP8GemmConfig("tile256", _lib.CONFIG_TILE256, 256, 256),
+    # One kernel variant each (tuning, and tests that reach every variant).
+    FP8GemmConfig("dma128x64", _lib.CONFIG_DMA128_64, 128, 64),
+    FP8GemmConfig("dma128x128", _lib.CONFIG_DMA128_128, 128, 128),
+    FP8GemmConfig("dma128x160", _lib.CONFIG_DMA128_160, 128, 160),
+    FP8GemmConfig("t256x128", _lib.CONFIG_T256_128, 256, 128),
+    FP8GemmConfig("t256x160", _lib.CONFIG_T256_160, 256, 160),
+    FP8GemmConfig("t256x192", _lib.CONFIG_T256_192, 256, 192),
+    FP8GemmConfig("t256x224", _lib.CONFIG_T256_224, 256, 224),
+    FP8GemmConfig("t256x256", _lib.CONFIG_T256_256, 256, 256),
 )
 # Alias under the reference's name.
 SPLIT_GEMM_CONFIGS = GEMM_CONFIGS

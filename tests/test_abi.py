@@ -39,6 +39,10 @@ def test_header_constants_match_binding():
                          "MI355X_FP8_ERR_INVALID": _lib.ERR_INVALID, "MI355X_FP8_ERR_UNSUPPORTED": _lib.ERR_UNSUPPORTED,
                          "MI355X_FP8_ERR_WORKSPACE": _lib.ERR_WORKSPACE, "MI355X_FP8_ERR_LAUNCH": _lib.ERR_LAUNCH,
                          "MI355X_FP8_ERR_SCRATCH": _lib.ERR_SCRATCH,
+                         "MI355X_FP8_CONFIG_DMA128_64": _lib.CONFIG_DMA128_64,
+                         "MI355X_FP8_CONFIG_DMA128_160": _lib.CONFIG_DMA128_160,
+                         "MI355X_FP8_CONFIG_T256_128": _lib.CONFIG_T256_128,
+                         "MI355X_FP8_CONFIG_T256_256": _lib.CONFIG_T256_256,
                          "MI355X_FP8_ABI_VERSION": _lib.ABI_VERSION}.items():
         assert re.search(rf"#define {macro} {value}\b", text), macro
 

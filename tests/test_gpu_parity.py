@@ -142,7 +142,7 @@ def test_linear_matches_oracle(gpu, shape, rows):
 @pytest.mark.parametrize("rows", [1, 16, 33, 130])
 def test_forced_configs_match_oracle_and_are_row_independent(gpu, config, shape, rows):
     _note("forced", config.name, shape, rows)
-    if config.name == "tile256" and shape.k % 128:
+    if config.needs_dma and shape.k % 128:
         pytest.skip("tile256 needs K % 128 == 0 (covered by test_tile256_rejects_unaligned_k)")
     x = make_activations(rows, shape.k, SEED)
     w, ws = make_weights(shape, SEED)
@@ -176,8 +176,8 @@ def test_tile256_tails(gpu, shape, rows):
 
 @pytest.mark.parametrize("config", fp8.GEMM_CONFIGS, ids=lambda c: c.name)
 def test_gemm_entry_on_prequantized_input(gpu, config):
-    if config.name == "tile256":
-        pytest.skip("tile256 needs K-group-major scales and K % 128 == 0")
+    if config.needs_dma:
+        pytest.skip("the LDS-DMA configs need K-group-major scales and K % 128 == 0")
     shape = ModelShape("tail", 193, 259)
     x = make_activations(40, shape.k, 5)
     w, ws = make_weights(shape, 5)
@@ -194,7 +194,7 @@ def test_gemm_entry_kgroup_scale_layout(gpu, config, shape, rows):
     """K-group-major scales (the layout the prefill kernel streams into LDS): same
     quantized values as the row layout, and the GEMM agrees with the oracle."""
 
-    if config.name == "tile256" and shape.k % 128:
+    if config.needs_dma and shape.k % 128:
         pytest.skip("tile256 needs K % 128 == 0")
     x = make_activations(rows, shape.k, 11)
     w, ws = make_weights(shape, 11)
@@ -401,7 +401,7 @@ def test_reference_gate_every_config_bitwise_and_row_independent(gpu, shape, row
         single = fp8.mi355x_fp8_linear(x[row:row + 1], wg, wsg, BLOCK, path="fused")
         assert bitwise_equal(single, reference[row:row + 1]), (row, bit_mismatch_details(single, reference[row:row + 1]))
     for config in fp8.GEMM_CONFIGS:
-        if config.name == "tile256" and shape.k % 128:
+        if config.needs_dma and shape.k % 128:
             continue
         actual = fp8.mi355x_fp8_linear(x, wg, wsg, BLOCK, path="split", gemm_config=config)
         assert bitwise_equal(reference, actual), f"{config.name}: {bit_mismatch_details(reference, actual)}"
@@ -476,7 +476,7 @@ def test_random_shapes_every_config_agrees(gpu):
         xg, wg, wsg = x.to(gpu), w.to(gpu), ws.to(gpu)
         auto = fp8.mi355x_fp8_linear(xg, wg, wsg, BLOCK)
         for config in fp8.GEMM_CONFIGS:
-            if config.name == "tile256" and k % 128:
+            if config.needs_dma and k % 128:
                 continue
             forced = fp8.mi355x_fp8_linear(xg, wg, wsg, BLOCK, path="split", gemm_config=config)
             assert bitwise_equal(auto, forced), (case, m, n, k, config.name, bit_mismatch_details(auto, forced))
