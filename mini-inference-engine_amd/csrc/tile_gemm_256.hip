@@ -165,8 +165,70 @@ struct Scales {
 // next K group (into the other stage, kn) go out in two halves, before the first and
 // before the middle MFMA group: a wave then never sits behind its whole DMA batch while
 // its partner wave on the SIMD does the same (measured 2-5 % faster than one batch).
+//
+// The fold is software-pipelined: column tile i's four MFMAs are issued, then tile i-1's
+// sixteen partials are folded while they run (one MFMA per four FMAs), so no fold waits on
+// the MFMA it follows.  The eight scale products a_s[j] * w_s (two weight-scale blocks at
+// most) are formed once per step; each is the same single fp32 product as before, so the
+// folded values are unchanged bit for bit.
 template <int BN, int NS, int S, int NXT>
 __device__ __forceinline__ void compute256(v4f (&acc)[Geo<BN>::kNI][4], const Scales& sc_in, uint32_t use_b, int wm,
+                                           int wn, int r, int g, const Src256& src, const uint8_t* w,
+                                           const uint8_t* q, int64_t kn, int wave) {
+  using G = Geo<BN>;
+  constexpr int NI = G::kNI;
+  constexpr int NDMA = G::kWPerWave + 4;
+  const uint4* st = stage256<NS, S>();
+  const int wrow0 = wn * (BN / 2) + r;
+  float sa[4], sb[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    sa[j] = sc_in.a[j] * sc_in.wa;
+    sb[j] = sc_in.a[j] * sc_in.wb;
+  }
+  v8i a0 = frag<S>(st, wrow0, g);
+  v8i b[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) b[j] = frag<S>(st + G::kXOff, wm * 64 + 16 * j + r, g);
+  v8i a1 = frag<S>(st, wrow0 + 16, g);
+  v4f p[2][4];
+#pragma unroll
+  for (int i = 0; i <= NI; ++i) {
+    if (i < NI) {
+#pragma unroll
+      for (int t = 0; t < NDMA; ++t)
+        if ((t < NDMA / 2 ? 0 : NI / 2) == i) issue_one<BN, NS, NXT>(src, w, q, kn, wave, t);
+      v8i a2;
+      if (i + 2 < NI) a2 = frag<S>(st, wrow0 + 16 * (i + 2), g);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) p[i & 1][j] = mfma_16x16x128_e4m3(a0, b[j]);
+      a0 = a1;
+      if (i + 2 < NI) a1 = a2;
+    }
+    if (i > 0) {
+      const int ip = i - 1;
+      const bool ub = (use_b >> ip) & 1;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float sc = ub ? sb[j] : sa[j];
+#pragma unroll
+        for (int v = 0; v < 4; ++v) acc[ip][j][v] = __builtin_fmaf(p[ip & 1][j][v], sc, acc[ip][j][v]);
+      }
+    }
+    if (i > 0 && i < NI) {
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
+      }
+    }
+  }
+}
+
+// The unpipelined fold, for the 256-wide tiles: their accumulators leave no registers for a
+// second set of partials (the pipelined form spills there).
+template <int BN, int NS, int S, int NXT>
+__device__ __forceinline__ void compute256_plain(v4f (&acc)[Geo<BN>::kNI][4], const Scales& sc_in, uint32_t use_b, int wm,
                                            int wn, int r, int g, const Src256& src, const uint8_t* w,
                                            const uint8_t* q, int64_t kn, int wave) {
   using G = Geo<BN>;
@@ -239,7 +301,10 @@ __device__ __forceinline__ void step256(v4f (&acc)[Geo<BN>::kNI][4], const Scale
   // Keep the scale loads ahead of the DMA loads (compiler and scheduler barriers).
   asm volatile("" ::: "memory");
   __builtin_amdgcn_sched_barrier(0);
-  compute256<BN, NS, CUR, (CUR + NS - 1) % NS>(acc, cur, src.use_b, wm, wn, r, g, src, w, q, kd, wave);
+  if constexpr (BN == 256)
+    compute256_plain<BN, NS, CUR, (CUR + NS - 1) % NS>(acc, cur, src.use_b, wm, wn, r, g, src, w, q, kd, wave);
+  else
+    compute256<BN, NS, CUR, (CUR + NS - 1) % NS>(acc, cur, src.use_b, wm, wn, r, g, src, w, q, kd, wave);
   // Every MFMA of the step is issued before the wait: the matrix core then works through
   // them while the wave waits for its DMA and the other waves (without this barrier the
   // scheduler moves the last MFMA groups behind s_barrier; measured 7 % slower on qkv).
