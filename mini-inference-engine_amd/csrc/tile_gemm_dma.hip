@@ -191,21 +191,18 @@ __device__ __forceinline__ void read_head(StepHead<BN>& h, const DmaSources& src
 
 // Folds column tile i's partials into the accumulator: acc = fma(p, as * ws, acc), ws being
 // the scale of the 128-column weight block the tile lies in.  Only BN = 160 lets a wave's
-// tiles straddle two blocks: there the tile's block scale is picked on the scalar unit and
-// its four scale products formed here; otherwise all tiles share the step's products sa.
+// tiles straddle two blocks; the step forms both blocks' four products once (sa, sb), and each
+// tile picks its block's set on the scalar unit.
 template <int BN>
-__device__ __forceinline__ void fold_tile(v4f (&acc)[DmaGeo<BN>::kNI][4], const v4f (&p)[4], const StepHead<BN>& h,
-                                          const float (&sa)[4], uint32_t use_b, int i) {
-  float sc[4];
+__device__ __forceinline__ void fold_tile(v4f (&acc)[DmaGeo<BN>::kNI][4], const v4f (&p)[4], const float (&sa)[4],
+                                          const float (&sb)[4], uint32_t use_b, int i) {
+  const bool ub = BN == 160 && ((use_b >> i) & 1);
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    if constexpr (BN == 160) sc[j] = h.as_v[j] * (((use_b >> i) & 1) ? h.wb : h.wa);
-    else sc[j] = sa[j];
+    const float sc = ub ? sb[j] : sa[j];
+#pragma unroll
+    for (int v = 0; v < 4; ++v) acc[i][j][v] = __builtin_fmaf(p[j][v], sc, acc[i][j][v]);
   }
-#pragma unroll
-  for (int j = 0; j < 4; ++j)
-#pragma unroll
-    for (int v = 0; v < 4; ++v) acc[i][j][v] = __builtin_fmaf(p[j][v], sc[j], acc[i][j][v]);
 }
 
 // One K group kb from stage CUR, whose head h was read during the previous step.
@@ -225,9 +222,12 @@ __device__ __forceinline__ void k_step(v4f (&acc)[DmaGeo<BN>::kNI][4], StepHead<
   constexpr int NB = NI >= 4 ? 2 : 1;  // weight fragments multiplied after the barrier
   constexpr int NA = NI - NB;
   constexpr int NXT = (CUR + 1) % STAGES;
-  float sa[4];
+  float sa[4], sb[4];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) sa[j] = h.as_v[j] * h.wa;
+  for (int j = 0; j < 4; ++j) {
+    sa[j] = h.as_v[j] * h.wa;
+    sb[j] = BN == 160 ? h.as_v[j] * h.wb : sa[j];
+  }
   v8i a[NI];
   a[0] = h.a0;
   v4f p[NI][4];
@@ -236,7 +236,7 @@ __device__ __forceinline__ void k_step(v4f (&acc)[DmaGeo<BN>::kNI][4], StepHead<
 #pragma unroll
     for (int j = 0; j < 4; ++j) p[i][j] = mfma_16x16x128_e4m3(a[i], h.b[j]);
     a[i + 1] = read_a<BN, CUR>(i + 1, wn, r, g);
-    if (i > 0) fold_tile<BN>(acc, p[i - 1], h, sa, src.use_b, i - 1);
+    if (i > 0) fold_tile<BN>(acc, p[i - 1], sa, sb, src.use_b, i - 1);
   }
 #pragma unroll
   for (int i = NA + 1; i < NI; ++i) a[i] = read_a<BN, CUR>(i, wn, r, g);
@@ -269,10 +269,10 @@ __device__ __forceinline__ void k_step(v4f (&acc)[DmaGeo<BN>::kNI][4], StepHead<
     p[i][j] = mfma_16x16x128_e4m3(a[i], h.b[j]);
 #pragma unroll
     for (int d = t * ND / NM; d < (t + 1) * ND / NM; ++d) issue_one<BN, CUR>(src, ahead, as_sk, wave, d);
-    if (j == 3 && i > 0) fold_tile<BN>(acc, p[i - 1], h, sa, src.use_b, i - 1);
+    if (j == 3 && i > 0) fold_tile<BN>(acc, p[i - 1], sa, sb, src.use_b, i - 1);
     __builtin_amdgcn_sched_barrier(0);
   }
-  fold_tile<BN>(acc, p[NI - 1], h, sa, src.use_b, NI - 1);
+  fold_tile<BN>(acc, p[NI - 1], sa, sb, src.use_b, NI - 1);
   __builtin_amdgcn_sched_barrier(0);
   h = nh;
 }
