@@ -194,33 +194,30 @@ __device__ __forceinline__ void compute256(v4f (&acc)[Geo<BN>::kNI][4], const Sc
   v4f p[2][4];
 #pragma unroll
   for (int i = 0; i <= NI; ++i) {
+    v8i a2;
     if (i < NI) {
 #pragma unroll
       for (int t = 0; t < NDMA; ++t)
         if ((t < NDMA / 2 ? 0 : NI / 2) == i) issue_one<BN, NS, NXT>(src, w, q, kn, wave, t);
-      v8i a2;
       if (i + 2 < NI) a2 = frag<S>(st, wrow0 + 16 * (i + 2), g);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) p[i & 1][j] = mfma_16x16x128_e4m3(a0, b[j]);
-      a0 = a1;
-      if (i + 2 < NI) a1 = a2;
     }
-    if (i > 0) {
-      const int ip = i - 1;
-      const bool ub = (use_b >> ip) & 1;
+    // MFMA (i, j), then the fold of (i - 1, j), whose MFMA went out four MFMAs earlier; the
+    // scheduling barriers keep that order, so no fold waits on the MFMA just issued.
+    const bool ub = i > 0 && ((use_b >> (i - 1)) & 1);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < 4; ++j) {
+      if (i < NI) p[i & 1][j] = mfma_16x16x128_e4m3(a0, b[j]);
+      if (i > 0) {
         const float sc = ub ? sb[j] : sa[j];
 #pragma unroll
-        for (int v = 0; v < 4; ++v) acc[ip][j][v] = __builtin_fmaf(p[ip & 1][j][v], sc, acc[ip][j][v]);
+        for (int v = 0; v < 4; ++v)
+          acc[i - 1][j][v] = __builtin_fmaf(p[(i - 1) & 1][j][v], sc, acc[i - 1][j][v]);
       }
+      __builtin_amdgcn_sched_barrier(0);
     }
-    if (i > 0 && i < NI) {
-#pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
-      }
+    if (i < NI) {
+      a0 = a1;
+      if (i + 2 < NI) a1 = a2;
     }
   }
 }
