@@ -439,9 +439,11 @@ int plan_gemm(int64_t M, int64_t N, int64_t K, int config, GemmPlan* plan) {
   // slices run side by side; 64-row slices re-read the activations 4x per workgroup instead
   // and measured slower (down at 40 rows 24.5 against 19.2 us).
   plan->token_tiles = M <= 16 ? 1 : 2;
-  // Two 16-row MFMA tiles per workgroup when N is wide enough to keep every CU busy
-  // anyway: halves the L2 re-reads of the activations.
-  plan->row_tiles = (N >= 16384 &&
+  // Two 16-row MFMA tiles per workgroup from N = 6144 up: halves the L2 re-reads of the
+  // activations.  Measured on the Qwen3-4B shapes: the merged qkv (N = 6144, 192 workgroups)
+  // 7.12 -> 6.78 us at 8 rows and 7.96 -> 7.14 us at 16, unchanged at 1 and 32 rows; o_proj
+  // and down (N = 2560) are slower with 80 workgroups and keep one tile.
+  plan->row_tiles = (N >= 6144 &&
                      stream_fold_bytes(cdiv(K, kGroup), 2, plan->token_tiles) <= kStreamFoldLds)
                         ? 2
                         : 1;
