@@ -66,3 +66,32 @@ def test_noalloc_rejects_calls_beyond_the_scratch(gpu):
         _lib.check(_lib.ERR_SCRATCH)
     torch.cuda.synchronize()
     assert (out == 7.0).all().item()  # nothing was launched
+
+
+def test_noalloc_under_hip_graph_capture(gpu):
+    """The no-allocation entry point captured in a HIP graph (the caller it exists for): every
+    replay, with eager work and synchronisations between them, gives the eager result."""
+
+    print("CASE noalloc graph", flush=True, file=sys.stderr)
+    x = make_activations(8, 2560, 41).to(gpu)
+    w, ws = make_weights(ModelShape("noalloc_graph", 6144, 2560), 41)
+    w, ws = w.to(gpu), ws.to(gpu)
+    ref = fp8.mi355x_fp8_linear(x, w, ws, [128, 128])
+    out = torch.full_like(ref, float("nan"))
+    stream = torch.cuda.Stream(gpu)
+    with torch.cuda.stream(stream):
+        _lib.check(_noalloc(x, w, ws, out))  # first call on the device outside capture
+        stream.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            _lib.check(_noalloc(x, w, ws, out))
+    for _ in range(3):
+        out.fill_(float("nan"))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert bitwise_equal(out, ref), bit_mismatch_details(out, ref)
+        # unrelated eager work between replays, through the same scratch
+        other = torch.empty_like(ref)
+        _lib.check(_noalloc(x[:3], w, ws, other[:3]))
+        torch.cuda.synchronize()
