@@ -46,6 +46,26 @@ def test_quantizer_bit_exact(gpu, k, rows, dtype):
     assert bitwise_equal(s.cpu(), s_ref), bit_mismatch_details(s.cpu(), s_ref)
 
 
+@pytest.mark.parametrize("rows,k", [(4100, 1000), (1640, 2560), (600, 9728), (4100, 1001)])
+@pytest.mark.parametrize("layout", ["row", "kgroup"])
+def test_quantizer_large_inputs(gpu, rows, k, layout):
+    """Large inputs (4-6 M elements, K tails of 104 and 105 elements): codes and scales
+    bit-exact with the oracle in either scale layout, and each sampled row alone gives the
+    batch's bits."""
+
+    _note("quant large", rows, k, layout)
+    x = make_activations(rows, k, SEED + 3)
+    xg = x.to(gpu)
+    q, s = fp8.quantize_mi355x_fp8_activation(xg, scale_layout=layout)
+    q_ref, s_ref = oracle_quant(x)
+    s_rows = s  # (M, groups) in either layout (a transposed view for kgroup)
+    assert bitwise_equal(q.cpu(), q_ref), bit_mismatch_details(q.cpu(), q_ref)
+    assert bitwise_equal(s_rows.cpu(), s_ref), bit_mismatch_details(s_rows.cpu(), s_ref)
+    for r in (0, 1, rows // 2, rows - 1):
+        q1, s1 = fp8.quantize_mi355x_fp8_activation(xg[r:r + 1])
+        assert bitwise_equal(q1, q[r:r + 1]) and bitwise_equal(s1, s_rows[r:r + 1]), r
+
+
 def test_quantizer_special_rows_and_row_independence(gpu):
     x = make_activations(7, 259, 42).to(gpu)
     q, scales = fp8.quantize_mi355x_fp8_activation(x)
