@@ -44,9 +44,16 @@ constexpr int kThreads = 256;  // tile kernel
 constexpr int kStreamWaves = 16;
 // One-round partial buffer limit: two workgroups of 1024 threads share a CU's 160 KiB.
 constexpr size_t kStreamFoldLds = 80 * 1024;
+// With at most one workgroup per CU (the five-tile form) the buffer may take most of the LDS.
+constexpr size_t kStreamFoldLdsOne = 144 * 1024;
+
+// Weight-scale rows one workgroup of af 16-row tiles needs per K group: one when its rows lie
+// in a single 128-row weight-scale block (af divides 8), else one per tile.
+__host__ __device__ constexpr int stream_scale_tiles(int af) { return 8 % af == 0 ? 1 : af; }
 
 __host__ __device__ constexpr size_t stream_fold_bytes(int64_t kb, int af, int nt) {
-  return static_cast<size_t>(kb) * (static_cast<size_t>(af) * nt * 256 + 16 * nt) * sizeof(float);
+  return static_cast<size_t>(kb) * (static_cast<size_t>(af) * nt * 256 + 16 * nt * stream_scale_tiles(af)) *
+         sizeof(float);
 }
 
 // The fold: the waves publish each K group's raw MFMA partials and the scale products
@@ -66,6 +73,7 @@ __global__ __launch_bounds__(kStreamWaves * 64) void stream_rounds_kernel(
     int64_t as_sk, const uint8_t* __restrict__ w, int64_t ldw, const float* __restrict__ ws,
     int64_t ws_sn, int64_t ws_sk, uint16_t* __restrict__ out, int64_t ldo, int64_t M, int64_t N,
     int64_t K, int64_t KB) {
+  static_assert(8 % AF == 0, "a workgroup's rows lie in one weight-scale block");
   constexpr int kRows = 16 * AF;  // W rows of this workgroup
   constexpr int kTok = 16 * NT;   // token rows of this slice
   constexpr int kBufs = AF * NT >= 4 ? 1 : 2;  // double-buffered publish when it fits
@@ -175,9 +183,9 @@ __global__ __launch_bounds__(kStreamWaves * 64) void stream_gemm_kernel(
     int64_t K, int64_t KB) {
   constexpr int kRows = 16 * AF;
   constexpr int kTok = 16 * NT;
-  constexpr int kTiles = AF * NT;
+  constexpr int kST = stream_scale_tiles(AF);
   // [KB][kTok][kRows] partials, element-major (the fold's reads are consecutive), then
-  // [KB][kTok] scale products.
+  // [KB][kST][kTok] scale products.
   float* part = reinterpret_cast<float*>(stream_fold_lds);
   float* scl = part + KB * kTok * kRows;
 
@@ -189,7 +197,14 @@ __global__ __launch_bounds__(kStreamWaves * 64) void stream_gemm_kernel(
   const int64_t n0 = static_cast<int64_t>(blockIdx.x) * kRows;
   const int64_t m_base = static_cast<int64_t>(blockIdx.z) * kTok;
   const int64_t m_rows = (M - m_base) < kTok ? (M - m_base) : kTok;
-  const int64_t nb = n0 / kGroup;
+  // Weight-scale block of each scale row (tiles past N take the last block: their rows
+  // read as zero and are never stored).
+  int64_t nb[kST];
+#pragma unroll
+  for (int i = 0; i < kST; ++i) {
+    const int64_t row = n0 + 16 * i < N ? n0 + 16 * i : N - 1;
+    nb[i] = row / kGroup;
+  }
   const int64_t wave_u = __builtin_amdgcn_readfirstlane(wave);
 
   // Operands of one K group in registers.  Waves keep two groups of loads in flight when
@@ -199,7 +214,7 @@ __global__ __launch_bounds__(kStreamWaves * 64) void stream_gemm_kernel(
   // the registers).
   struct Operands {
     v8i a[AF], b[NT];
-    float asv[NT], wsv;
+    float asv[NT], wsv[kST];
   };
   auto load = [&](Operands& o, int64_t kb) {
     const int64_t k_lo = kb * kGroup + 16 * g;
@@ -208,7 +223,8 @@ __global__ __launch_bounds__(kStreamWaves * 64) void stream_gemm_kernel(
       const int64_t row = n0 + 16 * i + r;
       o.a[i] = pack_v8i(load_chunk16<ALIGNED>(w, ldw, row, N, k_lo, K), load_chunk16<ALIGNED>(w, ldw, row, N, k_lo + 64, K));
     }
-    o.wsv = ws[nb * ws_sn + kb * ws_sk];
+#pragma unroll
+    for (int i = 0; i < kST; ++i) o.wsv[i] = ws[nb[i] * ws_sn + kb * ws_sk];
 #pragma unroll
     for (int j = 0; j < NT; ++j) {
       const int64_t tok = 16 * j + r;
@@ -225,9 +241,11 @@ __global__ __launch_bounds__(kStreamWaves * 64) void stream_gemm_kernel(
     for (int i = 0; i < AF; ++i)
 #pragma unroll
       for (int j = 0; j < NT; ++j) p[i][j] = mfma_16x16x128_e4m3(o.a[i], o.b[j]);
-    float sc[NT];
+    float sc[kST][NT];
 #pragma unroll
-    for (int j = 0; j < NT; ++j) sc[j] = o.asv[j] * o.wsv;
+    for (int i = 0; i < kST; ++i)
+#pragma unroll
+      for (int j = 0; j < NT; ++j) sc[i][j] = o.asv[j] * o.wsv[i];
     if (kb_next < KB) load(o, kb_next);
     // Lane holds D[n = 16 i + 4 g + v][tok = 16 j + r]: four consecutive n of one token.
 #pragma unroll
@@ -238,7 +256,9 @@ __global__ __launch_bounds__(kStreamWaves * 64) void stream_gemm_kernel(
             make_float4(p[i][j][0], p[i][j][1], p[i][j][2], p[i][j][3]);
     if (g == 0) {
 #pragma unroll
-      for (int j = 0; j < NT; ++j) scl[kb * kTok + 16 * j + r] = sc[j];
+      for (int i = 0; i < kST; ++i)
+#pragma unroll
+        for (int j = 0; j < NT; ++j) scl[(kb * kST + i) * kTok + 16 * j + r] = sc[i][j];
     }
   };
   constexpr int kDepth = ALIGNED && AF == 1 && NT == 1 ? 2 : 1;
@@ -255,27 +275,28 @@ __global__ __launch_bounds__(kStreamWaves * 64) void stream_gemm_kernel(
     }
   }
   __syncthreads();
-  const int e = tid;
-  if (e >= kRows * kTok) return;
-  const int tok = e / kRows, nl = e - (e / kRows) * kRows;
-  if (tok >= m_rows) return;  // padding token: nothing to fold
-  const float* pf = part + e;
-  const float* sf = scl + tok;
-  // Reads in batches of eight ahead of their FMAs, so the chain waits on LDS once per batch.
-  float acc = 0.0f;
-  int64_t kb = 0;
-  for (; kb + 8 <= KB; kb += 8) {
-    float pv[8], sv[8];
+  // One output element per thread (two for the five-tile workgroups).
+  for (int e = tid; e < kRows * kTok; e += kStreamWaves * 64) {
+    const int tok = e / kRows, nl = e - (e / kRows) * kRows;
+    if (tok >= m_rows) break;  // padding tokens: nothing to fold (later e only have larger tok)
+    const float* pf = part + e;
+    const float* sf = scl + (kST == 1 ? 0 : nl / 16) * kTok + tok;
+    // Reads in batches of eight ahead of their FMAs, so the chain waits on LDS once per batch.
+    float acc = 0.0f;
+    int64_t kb = 0;
+    for (; kb + 8 <= KB; kb += 8) {
+      float pv[8], sv[8];
 #pragma unroll
-    for (int x = 0; x < 8; ++x) {
-      pv[x] = pf[(kb + x) * kTok * kRows];
-      sv[x] = sf[(kb + x) * kTok];
+      for (int x = 0; x < 8; ++x) {
+        pv[x] = pf[(kb + x) * kTok * kRows];
+        sv[x] = sf[(kb + x) * kST * kTok];
+      }
+#pragma unroll
+      for (int x = 0; x < 8; ++x) acc = __builtin_fmaf(pv[x], sv[x], acc);
     }
-#pragma unroll
-    for (int x = 0; x < 8; ++x) acc = __builtin_fmaf(pv[x], sv[x], acc);
+    for (; kb < KB; ++kb) acc = __builtin_fmaf(pf[kb * kTok * kRows], sf[kb * kST * kTok], acc);
+    if (n0 + nl < N) out[(m_base + tok) * ldo + n0 + nl] = OutCvt<OutT>::cvt(acc);
   }
-  for (; kb < KB; ++kb) acc = __builtin_fmaf(pf[kb * kTok * kRows], sf[kb * kTok], acc);
-  if (n0 + nl < N) out[(m_base + tok) * ldo + n0 + nl] = OutCvt<OutT>::cvt(acc);
 }
 
 // ------------------------------------------------------------------------------------
@@ -447,6 +468,19 @@ int plan_gemm(int64_t M, int64_t N, int64_t K, int config, GemmPlan* plan) {
                      stream_fold_bytes(cdiv(K, kGroup), 2, plan->token_tiles) <= kStreamFoldLds)
                         ? 2
                         : 1;
+  // Five tiles (80 rows) per workgroup when that fits every workgroup on the chip at once
+  // and streams fewer weight rows per CU than the choice above.  A CU keeps only so many
+  // loads in flight, so the rows a CU streams bound the time: gate_up (N = 19456, 1216
+  // tiles) at two tiles gives 608 workgroups, 96 of them in a second round (six tiles on
+  // those CUs); at five tiles, 244 workgroups on 244 CUs stream five tiles each.
+  {
+    const int64_t tiles = cdiv(N, 16), cus = device_cus();
+    const int64_t wgs5 = cdiv(tiles, 5);
+    const int64_t cost = plan->row_tiles * cdiv(cdiv(tiles, plan->row_tiles), cus);
+    if (plan->token_tiles == 1 && wgs5 <= cus && 5 < cost &&
+        stream_fold_bytes(cdiv(K, kGroup), 5, 1) <= kStreamFoldLdsOne)
+      plan->row_tiles = 5;
+  }
   return MI355X_FP8_OK;
 }
 
@@ -543,12 +577,17 @@ static void launch_stream_t(const uint8_t* q, int64_t ldq, const float* as, int6
   dim3 grid(static_cast<unsigned>(cdiv(N, 16 * AF)), 1, static_cast<unsigned>(cdiv(M, 16 * NT)));
   const int64_t kb = cdiv(K, kGroup);
   const size_t one_round = stream_fold_bytes(kb, AF, NT);
-  if (one_round <= kStreamFoldLds)
+  if constexpr (8 % AF != 0) {
+    // Planned only when the one-round buffer fits (plan_gemm).
     stream_gemm_kernel<NT, AF, ALIGNED, OutT><<<grid, kStreamWaves * 64, one_round, stream>>>(
         q, ldq, as, as_sm, as_sk, w, ldw, ws, ws_sn, ws_sk, out, ldo, M, N, K, kb);
-  else
+  } else if (one_round <= kStreamFoldLds) {
+    stream_gemm_kernel<NT, AF, ALIGNED, OutT><<<grid, kStreamWaves * 64, one_round, stream>>>(
+        q, ldq, as, as_sm, as_sk, w, ldw, ws, ws_sn, ws_sk, out, ldo, M, N, K, kb);
+  } else {
     stream_rounds_kernel<NT, AF, ALIGNED, OutT><<<grid, kStreamWaves * 64, 0, stream>>>(
         q, ldq, as, as_sm, as_sk, w, ldw, ws, ws_sn, ws_sk, out, ldo, M, N, K, kb);
+  }
 }
 
 template <bool ALIGNED, typename OutT>
@@ -557,7 +596,9 @@ static void launch_stream(const GemmPlan& p, const uint8_t* q, int64_t ldq, cons
                           const float* ws, int64_t ws_sn, int64_t ws_sk, uint16_t* out, int64_t ldo,
                           int64_t M, int64_t N, int64_t K, hipStream_t stream) {
 #define MI355X_STREAM_ARGS q, ldq, as, as_sm, as_sk, w, ldw, ws, ws_sn, ws_sk, out, ldo, M, N, K, stream
-  if (p.token_tiles == 1)
+  if (p.token_tiles == 1 && p.row_tiles == 5)
+    launch_stream_t<1, 5, ALIGNED, OutT>(MI355X_STREAM_ARGS);
+  else if (p.token_tiles == 1)
     p.row_tiles == 2 ? launch_stream_t<1, 2, ALIGNED, OutT>(MI355X_STREAM_ARGS)
                      : launch_stream_t<1, 1, ALIGNED, OutT>(MI355X_STREAM_ARGS);
   else
