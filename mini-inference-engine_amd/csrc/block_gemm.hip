@@ -46,14 +46,13 @@ constexpr int kStreamWaves = 16;
 constexpr size_t kStreamFoldLds = 80 * 1024;
 // With at most one workgroup per CU (the five-tile form) the buffer may take most of the LDS.
 constexpr size_t kStreamFoldLdsOne = 144 * 1024;
+constexpr int64_t kStreamMinRows = 8;
 
-// Weight-scale rows one workgroup of af 16-row tiles needs per K group: one when its rows lie
-// in a single 128-row weight-scale block (af divides 8), else one per tile.
-__host__ __device__ constexpr int stream_scale_tiles(int af) { return 8 % af == 0 ? 1 : af; }
-
-__host__ __device__ constexpr size_t stream_fold_bytes(int64_t kb, int af, int nt) {
-  return static_cast<size_t>(kb) * (static_cast<size_t>(af) * nt * 256 + 16 * nt * stream_scale_tiles(af)) *
-         sizeof(float);
+// LDS of the one-round fold: the raw partials [KB][16 nt][16 af] and, per K group and token,
+// the scale products with the `blocks` (one, or two for ragged row counts) 128-row
+// weight-scale blocks a workgroup's rows touch.
+__host__ __device__ constexpr size_t stream_fold_bytes(int64_t kb, int af, int nt, int blocks = 1) {
+  return static_cast<size_t>(kb) * (static_cast<size_t>(af) * nt * 256 + blocks * 16 * nt) * sizeof(float);
 }
 
 // The fold: the waves publish each K group's raw MFMA partials and the scale products
@@ -173,19 +172,28 @@ __global__ __launch_bounds__(kStreamWaves * 64) void stream_rounds_kernel(
 // in LDS at once (dynamic LDS): each wave walks its K groups (w, w + 16, ...) with the
 // next group's loads in flight, publishes every partial, and after a single barrier one
 // thread per output element folds the whole K chain in order.
+//
+// RAGGED: a workgroup owns `rows` consecutive W rows (at most 16 AF; the MFMA tiles' rows
+// past them read as zero and are never stored), so the dispatch can give every CU the same
+// number of rows (a CU keeps only so many loads in flight, and the rows it streams set the
+// time).  The rows may then cross a 128-row weight-scale block: each K group publishes the
+// scale products with both blocks the rows touch, and the fold takes its row's.  Otherwise
+// a workgroup owns exactly 16 AF rows with 8 % AF == 0, inside one block.
 extern __shared__ float4 stream_fold_lds[];
 
-template <int NT, int AF, bool ALIGNED, typename OutT>
+template <int NT, int AF, bool ALIGNED, bool RAGGED, typename OutT>
 __global__ __launch_bounds__(kStreamWaves * 64) void stream_gemm_kernel(
     const uint8_t* __restrict__ q, int64_t ldq, const float* __restrict__ as, int64_t as_sm,
     int64_t as_sk, const uint8_t* __restrict__ w, int64_t ldw, const float* __restrict__ ws,
     int64_t ws_sn, int64_t ws_sk, uint16_t* __restrict__ out, int64_t ldo, int64_t M, int64_t N,
-    int64_t K, int64_t KB) {
+    int64_t K, int64_t KB, int rows_arg) {
+  static_assert(RAGGED || 8 % AF == 0, "a workgroup's rows lie in one weight-scale block");
   constexpr int kRows = 16 * AF;
   constexpr int kTok = 16 * NT;
-  constexpr int kST = stream_scale_tiles(AF);
+  constexpr int kSB = RAGGED ? 2 : 1;
+  const int rows = RAGGED ? rows_arg : kRows;
   // [KB][kTok][kRows] partials, element-major (the fold's reads are consecutive), then
-  // [KB][kST][kTok] scale products.
+  // [KB][kSB][kTok] scale products (first and last weight-scale block of the rows).
   float* part = reinterpret_cast<float*>(stream_fold_lds);
   float* scl = part + KB * kTok * kRows;
 
@@ -194,17 +202,11 @@ __global__ __launch_bounds__(kStreamWaves * 64) void stream_gemm_kernel(
   const int lane = tid & 63;
   const int r = lane & 15;
   const int g = lane >> 4;
-  const int64_t n0 = static_cast<int64_t>(blockIdx.x) * kRows;
+  const int64_t n0 = static_cast<int64_t>(blockIdx.x) * rows;
+  const int64_t n_end = n0 + rows < N ? n0 + rows : N;
   const int64_t m_base = static_cast<int64_t>(blockIdx.z) * kTok;
   const int64_t m_rows = (M - m_base) < kTok ? (M - m_base) : kTok;
-  // Weight-scale block of each scale row (tiles past N take the last block: their rows
-  // read as zero and are never stored).
-  int64_t nb[kST];
-#pragma unroll
-  for (int i = 0; i < kST; ++i) {
-    const int64_t row = n0 + 16 * i < N ? n0 + 16 * i : N - 1;
-    nb[i] = row / kGroup;
-  }
+  const int64_t nb0 = n0 / kGroup, nb1 = (n_end - 1) / kGroup;
   const int64_t wave_u = __builtin_amdgcn_readfirstlane(wave);
 
   // Operands of one K group in registers.  Waves keep two groups of loads in flight when
@@ -214,17 +216,18 @@ __global__ __launch_bounds__(kStreamWaves * 64) void stream_gemm_kernel(
   // the registers).
   struct Operands {
     v8i a[AF], b[NT];
-    float asv[NT], wsv[kST];
+    float asv[NT], wsv[kSB];
   };
   auto load = [&](Operands& o, int64_t kb) {
     const int64_t k_lo = kb * kGroup + 16 * g;
 #pragma unroll
     for (int i = 0; i < AF; ++i) {
       const int64_t row = n0 + 16 * i + r;
-      o.a[i] = pack_v8i(load_chunk16<ALIGNED>(w, ldw, row, N, k_lo, K), load_chunk16<ALIGNED>(w, ldw, row, N, k_lo + 64, K));
+      o.a[i] = pack_v8i(load_chunk16<ALIGNED>(w, ldw, row, RAGGED ? n_end : N, k_lo, K),
+                        load_chunk16<ALIGNED>(w, ldw, row, RAGGED ? n_end : N, k_lo + 64, K));
     }
-#pragma unroll
-    for (int i = 0; i < kST; ++i) o.wsv[i] = ws[nb[i] * ws_sn + kb * ws_sk];
+    o.wsv[0] = ws[nb0 * ws_sn + kb * ws_sk];
+    if constexpr (RAGGED) o.wsv[kSB - 1] = ws[nb1 * ws_sn + kb * ws_sk];
 #pragma unroll
     for (int j = 0; j < NT; ++j) {
       const int64_t tok = 16 * j + r;
@@ -241,11 +244,11 @@ __global__ __launch_bounds__(kStreamWaves * 64) void stream_gemm_kernel(
     for (int i = 0; i < AF; ++i)
 #pragma unroll
       for (int j = 0; j < NT; ++j) p[i][j] = mfma_16x16x128_e4m3(o.a[i], o.b[j]);
-    float sc[kST][NT];
+    float sc[kSB][NT];
 #pragma unroll
-    for (int i = 0; i < kST; ++i)
+    for (int b = 0; b < kSB; ++b)
 #pragma unroll
-      for (int j = 0; j < NT; ++j) sc[i][j] = o.asv[j] * o.wsv[i];
+      for (int j = 0; j < NT; ++j) sc[b][j] = o.asv[j] * o.wsv[b];
     if (kb_next < KB) load(o, kb_next);
     // Lane holds D[n = 16 i + 4 g + v][tok = 16 j + r]: four consecutive n of one token.
 #pragma unroll
@@ -256,9 +259,9 @@ __global__ __launch_bounds__(kStreamWaves * 64) void stream_gemm_kernel(
             make_float4(p[i][j][0], p[i][j][1], p[i][j][2], p[i][j][3]);
     if (g == 0) {
 #pragma unroll
-      for (int i = 0; i < kST; ++i)
+      for (int b = 0; b < kSB; ++b)
 #pragma unroll
-        for (int j = 0; j < NT; ++j) scl[(kb * kST + i) * kTok + 16 * j + r] = sc[i][j];
+        for (int j = 0; j < NT; ++j) scl[(kb * kSB + b) * kTok + 16 * j + r] = sc[b][j];
     }
   };
   constexpr int kDepth = ALIGNED && AF == 1 && NT == 1 ? 2 : 1;
@@ -275,12 +278,13 @@ __global__ __launch_bounds__(kStreamWaves * 64) void stream_gemm_kernel(
     }
   }
   __syncthreads();
-  // One output element per thread (two for the five-tile workgroups).
-  for (int e = tid; e < kRows * kTok; e += kStreamWaves * 64) {
-    const int tok = e / kRows, nl = e - (e / kRows) * kRows;
+  // One output element (token, row) per thread, two when rows x tokens exceeds the threads.
+  const int live = RAGGED ? static_cast<int>(n_end - n0) : kRows;
+  for (int e = tid; e < live * kTok; e += kStreamWaves * 64) {
+    const int tok = e / live, nl = e - (e / live) * live;
     if (tok >= m_rows) break;  // padding tokens: nothing to fold (later e only have larger tok)
-    const float* pf = part + e;
-    const float* sf = scl + (kST == 1 ? 0 : nl / 16) * kTok + tok;
+    const float* pf = part + tok * kRows + nl;
+    const float* sf = scl + (RAGGED && (n0 + nl) / kGroup != nb0 ? kTok : 0) + tok;
     // Reads in batches of eight ahead of their FMAs, so the chain waits on LDS once per batch.
     float acc = 0.0f;
     int64_t kb = 0;
@@ -289,13 +293,13 @@ __global__ __launch_bounds__(kStreamWaves * 64) void stream_gemm_kernel(
 #pragma unroll
       for (int x = 0; x < 8; ++x) {
         pv[x] = pf[(kb + x) * kTok * kRows];
-        sv[x] = sf[(kb + x) * kST * kTok];
+        sv[x] = sf[(kb + x) * kSB * kTok];
       }
 #pragma unroll
       for (int x = 0; x < 8; ++x) acc = __builtin_fmaf(pv[x], sv[x], acc);
     }
-    for (; kb < KB; ++kb) acc = __builtin_fmaf(pf[kb * kTok * kRows], sf[kb * kST * kTok], acc);
-    if (n0 + nl < N) out[(m_base + tok) * ldo + n0 + nl] = OutCvt<OutT>::cvt(acc);
+    for (; kb < KB; ++kb) acc = __builtin_fmaf(pf[kb * kTok * kRows], sf[kb * kSB * kTok], acc);
+    if (RAGGED || n0 + nl < N) out[(m_base + tok) * ldo + n0 + nl] = OutCvt<OutT>::cvt(acc);
   }
 }
 
@@ -468,18 +472,27 @@ int plan_gemm(int64_t M, int64_t N, int64_t K, int config, GemmPlan* plan) {
                      stream_fold_bytes(cdiv(K, kGroup), 2, plan->token_tiles) <= kStreamFoldLds)
                         ? 2
                         : 1;
-  // Five tiles (80 rows) per workgroup when that fits every workgroup on the chip at once
-  // and streams fewer weight rows per CU than the choice above.  A CU keeps only so many
-  // loads in flight, so the rows a CU streams bound the time: gate_up (N = 19456, 1216
-  // tiles) at two tiles gives 608 workgroups, 96 of them in a second round (six tiles on
-  // those CUs); at five tiles, 244 workgroups on 244 CUs stream five tiles each.
-  {
-    const int64_t tiles = cdiv(N, 16), cus = device_cus();
-    const int64_t wgs5 = cdiv(tiles, 5);
-    const int64_t cost = plan->row_tiles * cdiv(cdiv(tiles, plan->row_tiles), cus);
-    if (plan->token_tiles == 1 && wgs5 <= cus && 5 < cost &&
-        stream_fold_bytes(cdiv(K, kGroup), 5, 1) <= kStreamFoldLdsOne)
-      plan->row_tiles = 5;
+  plan->rows = 16 * plan->row_tiles;
+  // Up to 16 tokens: the same number of weight rows on every CU, one workgroup per CU, when
+  // that fits in five MFMA tiles and the LDS, and either a workgroup then holds one MFMA tile
+  // or the 16-row-multiple plan needs more workgroups than CUs.  A CU keeps only so many loads
+  // in flight, so the rows it streams matter; every workgroup also re-reads all of the
+  // activations, which is why spreading a plan that already runs in one round does not pay
+  // for two-tile workgroups.
+  // Measured at M = 8 (Qwen3-4B): o_proj 16 -> 10 rows per CU 6.25 -> 5.99 us, down 16 -> 10
+  // 10.1 -> 9.7 us, gate_up 96 (three 32-row workgroups on some CUs) -> 76 14.7 -> 12.7 us;
+  // qkv 32 -> 24 measured 6.84 -> 6.93 us and keeps 32.  At least kStreamMinRows rows per
+  // workgroup, so that narrow weights do not spread over workgroups for a few rows each.
+  if (plan->token_tiles == 1) {
+    const int64_t cus = device_cus();
+    const int64_t rows = cdiv(N, cus) > kStreamMinRows ? cdiv(N, cus) : kStreamMinRows;
+    const int64_t af = cdiv(rows, 16);
+    const int64_t old_rows = plan->rows * cdiv(cdiv(N, plan->rows), cus);
+    if (af <= 5 && cdiv(N, rows) <= cus && rows < old_rows && (af == 1 || cdiv(N, plan->rows) > cus) &&
+        stream_fold_bytes(cdiv(K, kGroup), static_cast<int>(af), 1, 2) <= kStreamFoldLdsOne) {
+      plan->row_tiles = static_cast<int>(af);
+      plan->rows = static_cast<int>(rows);
+    }
   }
   return MI355X_FP8_OK;
 }
@@ -573,21 +586,25 @@ int tile256_width(int64_t M, int64_t N, int64_t cus) {
 template <int NT, int AF, bool ALIGNED, typename OutT>
 static void launch_stream_t(const uint8_t* q, int64_t ldq, const float* as, int64_t as_sm, int64_t as_sk,
                             const uint8_t* w, int64_t ldw, const float* ws, int64_t ws_sn, int64_t ws_sk,
-                            uint16_t* out, int64_t ldo, int64_t M, int64_t N, int64_t K, hipStream_t stream) {
-  dim3 grid(static_cast<unsigned>(cdiv(N, 16 * AF)), 1, static_cast<unsigned>(cdiv(M, 16 * NT)));
+                            uint16_t* out, int64_t ldo, int64_t M, int64_t N, int64_t K, int rows,
+                            hipStream_t stream) {
+  dim3 grid(static_cast<unsigned>(cdiv(N, rows)), 1, static_cast<unsigned>(cdiv(M, 16 * NT)));
   const int64_t kb = cdiv(K, kGroup);
-  const size_t one_round = stream_fold_bytes(kb, AF, NT);
-  if constexpr (8 % AF != 0) {
-    // Planned only when the one-round buffer fits (plan_gemm).
-    stream_gemm_kernel<NT, AF, ALIGNED, OutT><<<grid, kStreamWaves * 64, one_round, stream>>>(
-        q, ldq, as, as_sm, as_sk, w, ldw, ws, ws_sn, ws_sk, out, ldo, M, N, K, kb);
-  } else if (one_round <= kStreamFoldLds) {
-    stream_gemm_kernel<NT, AF, ALIGNED, OutT><<<grid, kStreamWaves * 64, one_round, stream>>>(
-        q, ldq, as, as_sm, as_sk, w, ldw, ws, ws_sn, ws_sk, out, ldo, M, N, K, kb);
-  } else {
-    stream_rounds_kernel<NT, AF, ALIGNED, OutT><<<grid, kStreamWaves * 64, 0, stream>>>(
-        q, ldq, as, as_sm, as_sk, w, ldw, ws, ws_sn, ws_sk, out, ldo, M, N, K, kb);
+  // Ragged row counts are planned only where the one-round buffer fits (plan_gemm).
+  if constexpr (8 % AF == 0) {
+    if (rows == 16 * AF) {
+      const size_t one_round = stream_fold_bytes(kb, AF, NT);
+      if (one_round <= kStreamFoldLds)
+        stream_gemm_kernel<NT, AF, ALIGNED, false, OutT><<<grid, kStreamWaves * 64, one_round, stream>>>(
+            q, ldq, as, as_sm, as_sk, w, ldw, ws, ws_sn, ws_sk, out, ldo, M, N, K, kb, rows);
+      else
+        stream_rounds_kernel<NT, AF, ALIGNED, OutT><<<grid, kStreamWaves * 64, 0, stream>>>(
+            q, ldq, as, as_sm, as_sk, w, ldw, ws, ws_sn, ws_sk, out, ldo, M, N, K, kb);
+      return;
+    }
   }
+  stream_gemm_kernel<NT, AF, ALIGNED, true, OutT><<<grid, kStreamWaves * 64, stream_fold_bytes(kb, AF, NT, 2), stream>>>(
+      q, ldq, as, as_sm, as_sk, w, ldw, ws, ws_sn, ws_sk, out, ldo, M, N, K, kb, rows);
 }
 
 template <bool ALIGNED, typename OutT>
@@ -595,15 +612,19 @@ static void launch_stream(const GemmPlan& p, const uint8_t* q, int64_t ldq, cons
                           int64_t as_sm, int64_t as_sk, const uint8_t* w, int64_t ldw,
                           const float* ws, int64_t ws_sn, int64_t ws_sk, uint16_t* out, int64_t ldo,
                           int64_t M, int64_t N, int64_t K, hipStream_t stream) {
-#define MI355X_STREAM_ARGS q, ldq, as, as_sm, as_sk, w, ldw, ws, ws_sn, ws_sk, out, ldo, M, N, K, stream
-  if (p.token_tiles == 1 && p.row_tiles == 5)
-    launch_stream_t<1, 5, ALIGNED, OutT>(MI355X_STREAM_ARGS);
-  else if (p.token_tiles == 1)
-    p.row_tiles == 2 ? launch_stream_t<1, 2, ALIGNED, OutT>(MI355X_STREAM_ARGS)
-                     : launch_stream_t<1, 1, ALIGNED, OutT>(MI355X_STREAM_ARGS);
-  else
+#define MI355X_STREAM_ARGS q, ldq, as, as_sm, as_sk, w, ldw, ws, ws_sn, ws_sk, out, ldo, M, N, K, p.rows, stream
+  if (p.token_tiles == 1) {
+    switch (p.row_tiles) {
+      case 5: launch_stream_t<1, 5, ALIGNED, OutT>(MI355X_STREAM_ARGS); break;
+      case 4: launch_stream_t<1, 4, ALIGNED, OutT>(MI355X_STREAM_ARGS); break;
+      case 3: launch_stream_t<1, 3, ALIGNED, OutT>(MI355X_STREAM_ARGS); break;
+      case 2: launch_stream_t<1, 2, ALIGNED, OutT>(MI355X_STREAM_ARGS); break;
+      default: launch_stream_t<1, 1, ALIGNED, OutT>(MI355X_STREAM_ARGS); break;
+    }
+  } else {
     p.row_tiles == 2 ? launch_stream_t<2, 2, ALIGNED, OutT>(MI355X_STREAM_ARGS)
                      : launch_stream_t<2, 1, ALIGNED, OutT>(MI355X_STREAM_ARGS);
+  }
 #undef MI355X_STREAM_ARGS
 }
 
@@ -624,7 +645,8 @@ static int launch_typed(const GemmPlan& plan, const uint8_t* q, int64_t ldq, con
                         int64_t ws_sn, int64_t ws_sk, uint16_t* out, int64_t ldo, int64_t M, int64_t N,
                         int64_t K, void* workspace, hipStream_t stream) {
   if (plan.kernel == MI355X_FP8_CONFIG_STREAM) {
-    if (cdiv(N, 16) > 0x7fffffffLL || cdiv(M, 16 * plan.token_tiles) > 65535) return MI355X_FP8_ERR_UNSUPPORTED;
+    if (plan.rows < 1 || cdiv(N, plan.rows) > 0x7fffffffLL || cdiv(M, 16 * plan.token_tiles) > 65535)
+      return MI355X_FP8_ERR_UNSUPPORTED;
     launch_stream<ALIGNED, OutT>(plan, q, ldq, as, as_sm, as_sk, w, ldw, ws, ws_sn, ws_sk, out, ldo, M, N, K,
                                  stream);
   } else {

@@ -28,7 +28,8 @@ int rmsnorm_block_width(int64_t rows, int64_t K);
 struct GemmPlan {
   int kernel;       // MI355X_FP8_CONFIG_STREAM or MI355X_FP8_CONFIG_TILE128
   int token_tiles;  // stream kernel: 16-token MFMA tiles per slice (1 or 2)
-  int row_tiles;    // stream kernel: 16-row MFMA tiles of W per workgroup (1, 2 or 5)
+  int row_tiles;    // stream kernel: 16-row MFMA tiles of W per workgroup (1 to 5)
+  int rows;         // stream kernel: W rows per workgroup (at most 16 row_tiles)
 };
 
 int plan_gemm(int64_t M, int64_t N, int64_t K, int config, GemmPlan* plan);
