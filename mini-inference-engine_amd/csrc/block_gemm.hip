@@ -473,7 +473,7 @@ int plan_gemm(int64_t M, int64_t N, int64_t K, int config, GemmPlan* plan) {
                         ? 2
                         : 1;
   plan->rows = 16 * plan->row_tiles;
-  // Up to 16 tokens: the same number of weight rows on every CU, one workgroup per CU, when
+  // The same number of weight rows on every CU, one workgroup per CU and token slice, when
   // that fits in five MFMA tiles and the LDS, and either a workgroup then holds one MFMA tile
   // or the 16-row-multiple plan needs more workgroups than CUs.  A CU keeps only so many loads
   // in flight, so the rows it streams matter; every workgroup also re-reads all of the
@@ -483,13 +483,15 @@ int plan_gemm(int64_t M, int64_t N, int64_t K, int config, GemmPlan* plan) {
   // 10.1 -> 9.7 us, gate_up 96 (three 32-row workgroups on some CUs) -> 76 14.7 -> 12.7 us;
   // qkv 32 -> 24 measured 6.84 -> 6.93 us and keeps 32.  At least kStreamMinRows rows per
   // workgroup, so that narrow weights do not spread over workgroups for a few rows each.
-  if (plan->token_tiles == 1) {
-    const int64_t cus = device_cus();
-    const int64_t rows = cdiv(N, cus) > kStreamMinRows ? cdiv(N, cus) : kStreamMinRows;
+  {
+    const int64_t slices = cdiv(M, 16 * plan->token_tiles);
+    const int64_t cus = device_cus(), share = cus / slices > 1 ? cus / slices : 1;
+    const int64_t rows = cdiv(N, share) > kStreamMinRows ? cdiv(N, share) : kStreamMinRows;
     const int64_t af = cdiv(rows, 16);
-    const int64_t old_rows = plan->rows * cdiv(cdiv(N, plan->rows), cus);
-    if (af <= 5 && cdiv(N, rows) <= cus && rows < old_rows && (af == 1 || cdiv(N, plan->rows) > cus) &&
-        stream_fold_bytes(cdiv(K, kGroup), static_cast<int>(af), 1, 2) <= kStreamFoldLdsOne) {
+    const int64_t old_wgs = cdiv(N, plan->rows) * slices;
+    const int64_t old_rows = plan->rows * cdiv(old_wgs, cus);
+    if (af <= 5 && cdiv(N, rows) * slices <= cus && rows < old_rows && (af == 1 || old_wgs > cus) &&
+        stream_fold_bytes(cdiv(K, kGroup), static_cast<int>(af), plan->token_tiles, 2) <= kStreamFoldLdsOne) {
       plan->row_tiles = static_cast<int>(af);
       plan->rows = static_cast<int>(rows);
     }
@@ -622,8 +624,13 @@ static void launch_stream(const GemmPlan& p, const uint8_t* q, int64_t ldq, cons
       default: launch_stream_t<1, 1, ALIGNED, OutT>(MI355X_STREAM_ARGS); break;
     }
   } else {
-    p.row_tiles == 2 ? launch_stream_t<2, 2, ALIGNED, OutT>(MI355X_STREAM_ARGS)
-                     : launch_stream_t<2, 1, ALIGNED, OutT>(MI355X_STREAM_ARGS);
+    switch (p.row_tiles) {
+      case 5: launch_stream_t<2, 5, ALIGNED, OutT>(MI355X_STREAM_ARGS); break;
+      case 4: launch_stream_t<2, 4, ALIGNED, OutT>(MI355X_STREAM_ARGS); break;
+      case 3: launch_stream_t<2, 3, ALIGNED, OutT>(MI355X_STREAM_ARGS); break;
+      case 2: launch_stream_t<2, 2, ALIGNED, OutT>(MI355X_STREAM_ARGS); break;
+      default: launch_stream_t<2, 1, ALIGNED, OutT>(MI355X_STREAM_ARGS); break;
+    }
   }
 #undef MI355X_STREAM_ARGS
 }
