@@ -108,7 +108,10 @@ size_t mi355x_fp8_linear_workspace_bytes(int64_t M, int64_t N, int64_t K, int co
 /*
  * The full linear: quantize x, then the block GEMM.  Replaces the kernel launches of
  * sm89_fp8_linear (engine/kernels/sm89_fp8.py:488-526); the Python wrapper keeps the
- * reference's validation, reshaping and bias handling.  Arguments as above.
+ * reference's validation, reshaping and bias handling.  Arguments as above.  At decode
+ * sizes with short K (M <= 16, K <= 3072, K % 16 == 0, 16-byte aligned rows) it is one
+ * launch that quantizes inside the GEMM, like the reference's fused path; the workspace is
+ * then untouched.  Either way the output bits are the same.
  */
 int mi355x_fp8_linear(const void* x, int x_dtype, int64_t M, int64_t K, int64_t sxm,
                       int64_t sxk, const uint8_t* w, int64_t ldw, const float* ws,

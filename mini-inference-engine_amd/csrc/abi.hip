@@ -161,6 +161,10 @@ int mi355x_fp8_linear(const void* x, int x_dtype, int64_t M, int64_t K, int64_t 
   if (!x || !w || !ws || !out) return MI355X_FP8_ERR_INVALID;
   if (workspace == nullptr || workspace_bytes < L.total) return MI355X_FP8_ERR_WORKSPACE;
   hipStream_t s = static_cast<hipStream_t>(stream);
+  // Decode sizes: one launch, the stream kernel quantizing its own K groups (same codes,
+  // scales and output bits as the two launches below).
+  st = launch_linear_stream(L.plan, x, x_dtype, sxm, sxk, w, ldw, ws, ws_sn, ws_sk, out, out_dtype, ldo, M, N, K, s);
+  if (st != MI355X_FP8_ERR_UNSUPPORTED) return st;
   char* base = static_cast<char*>(workspace);
   uint8_t* q = reinterpret_cast<uint8_t*>(base + L.q_off);
   float* as = reinterpret_cast<float*>(base + L.s_off);

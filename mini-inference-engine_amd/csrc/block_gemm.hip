@@ -29,6 +29,8 @@
 #include "fp8_abi_internal.h"
 #include "fp8_common.h"
 
+#include <type_traits>
+
 namespace mi355x {
 
 constexpr int kThreads = 256;  // tile kernel
@@ -181,13 +183,21 @@ __global__ __launch_bounds__(kStreamWaves * 64) void stream_rounds_kernel(
 // a workgroup owns exactly 16 AF rows with 8 % AF == 0, inside one block.
 extern __shared__ float4 stream_fold_lds[];
 
-template <int NT, int AF, bool ALIGNED, bool RAGGED, typename OutT>
+template <int NT, int AF, bool ALIGNED, bool RAGGED, typename OutT, typename XIn = uint8_t>
 __global__ __launch_bounds__(kStreamWaves * 64) void stream_gemm_kernel(
     const uint8_t* __restrict__ q, int64_t ldq, const float* __restrict__ as, int64_t as_sm,
     int64_t as_sk, const uint8_t* __restrict__ w, int64_t ldw, const float* __restrict__ ws,
     int64_t ws_sn, int64_t ws_sk, uint16_t* __restrict__ out, int64_t ldo, int64_t M, int64_t N,
     int64_t K, int64_t KB, int rows_arg) {
   static_assert(RAGGED || 8 % AF == 0, "a workgroup's rows lie in one weight-scale block");
+  // XIn = uint8_t: q holds the quantized activations (ldq bytes per row) and as their scales.
+  // XIn = bf16_t / f16_t: q holds the unquantized activations (ldq elements per row, 16-byte
+  // aligned rows, K % 16 == 0) and each wave quantizes its own K groups in registers, with
+  // the quantizer's arithmetic (quant_group16's amax, scale and codes), so the codes and
+  // scales, and therefore the output bits, are those of the two-launch path.
+  constexpr bool kQuant = !std::is_same<XIn, uint8_t>::value;
+  using XT = typename std::conditional<kQuant, XIn, bf16_t>::type;  // element type when quantizing
+  static_assert(!kQuant || (ALIGNED && NT == 1), "in-kernel quantization: aligned, one token tile");
   constexpr int kRows = 16 * AF;
   constexpr int kTok = 16 * NT;
   constexpr int kSB = RAGGED ? 2 : 1;
@@ -217,6 +227,7 @@ __global__ __launch_bounds__(kStreamWaves * 64) void stream_gemm_kernel(
   struct Operands {
     v8i a[AF], b[NT];
     float asv[NT], wsv[kSB];
+    uint4 xr[kQuant ? 4 : 1];  // unquantized activations: elements 16 g .. +15 and 64 + 16 g .. +15
   };
   auto load = [&](Operands& o, int64_t kb) {
     const int64_t k_lo = kb * kGroup + 16 * g;
@@ -228,17 +239,54 @@ __global__ __launch_bounds__(kStreamWaves * 64) void stream_gemm_kernel(
     }
     o.wsv[0] = ws[nb0 * ws_sn + kb * ws_sk];
     if constexpr (RAGGED) o.wsv[kSB - 1] = ws[nb1 * ws_sn + kb * ws_sk];
+    if constexpr (kQuant) {
+      const int64_t m = m_base + r;
+      const XT* xrow = reinterpret_cast<const XT*>(q) + m * ldq;
 #pragma unroll
-    for (int j = 0; j < NT; ++j) {
-      const int64_t tok = 16 * j + r;
-      const int64_t m = m_base + tok;
-      o.b[j] = pack_v8i(load_chunk16<ALIGNED>(q, ldq, m, M, k_lo, K), load_chunk16<ALIGNED>(q, ldq, m, M, k_lo + 64, K));
-      o.asv[j] = tok < m_rows ? as[m * as_sm + kb * as_sk] : 0.0f;
+      for (int c = 0; c < 4; ++c) {
+        const int64_t k = k_lo + 64 * (c >> 1) + 8 * (c & 1);
+        o.xr[c] = (r < m_rows && k < K) ? *reinterpret_cast<const uint4*>(xrow + k) : make_uint4(0u, 0u, 0u, 0u);
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < NT; ++j) {
+        const int64_t tok = 16 * j + r;
+        const int64_t m = m_base + tok;
+        o.b[j] = pack_v8i(load_chunk16<ALIGNED>(q, ldq, m, M, k_lo, K), load_chunk16<ALIGNED>(q, ldq, m, M, k_lo + 64, K));
+        o.asv[j] = tok < m_rows ? as[m * as_sm + kb * as_sk] : 0.0f;
+      }
     }
+  };
+  // The 1x128 quantizer on the lane's 32 elements of its token's K group; the four lanes of a
+  // token (g = 0..3) hold the whole group, so the amax takes two cross-lane steps.
+  auto quantize = [&](Operands& o) {
+    float t[32];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const uint32_t wv[4] = {o.xr[c].x, o.xr[c].y, o.xr[c].z, o.xr[c].w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        t[8 * c + 2 * e] = to_f32(XT{static_cast<uint16_t>(wv[e] & 0xffffu)});
+        t[8 * c + 2 * e + 1] = to_f32(XT{static_cast<uint16_t>(wv[e] >> 16)});
+      }
+    }
+    float amax = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 32; ++e) amax = fmaxf(amax, fabsf(t[e]));
+    amax = fmaxf(amax, __shfl_xor(amax, 16));
+    amax = fmaxf(amax, __shfl_xor(amax, 32));
+    const float scale = amax / 448.0f;
+    const float den = scale > 1e-12f ? scale : 1e-12f;
+    uint32_t packed[8];
+    quant_codes<32>(t, den, packed);
+    o.b[0] = pack_v8i(make_uint4(packed[0], packed[1], packed[2], packed[3]),
+                      make_uint4(packed[4], packed[5], packed[6], packed[7]));
+    o.asv[0] = scale;
   };
   // MFMA partials of group kb and their publication; `refill` loads group kb_next into the
   // registers just consumed (issued before the LDS writes, so it overlaps them).
   auto consume = [&](Operands& o, int64_t kb, int64_t kb_next) {
+    if constexpr (kQuant) quantize(o);
     v4f p[AF][NT];
 #pragma unroll
     for (int i = 0; i < AF; ++i)
@@ -701,6 +749,75 @@ int launch_block_gemm(const GemmPlan& plan, const uint8_t* q, int64_t ldq, const
     return out_dtype == kBF16 ? launch_typed<true, bf16_t>(MI355X_GEMM_ARGS) : launch_typed<true, f16_t>(MI355X_GEMM_ARGS);
   return out_dtype == kBF16 ? launch_typed<false, bf16_t>(MI355X_GEMM_ARGS) : launch_typed<false, f16_t>(MI355X_GEMM_ARGS);
 #undef MI355X_GEMM_ARGS
+}
+
+// The whole linear in one launch at decode sizes: the stream kernel quantizing its own K
+// groups (XIn = bf16_t / f16_t).  Returns MI355X_FP8_ERR_UNSUPPORTED, having launched
+// nothing, when the call does not fit that form (then the caller quantizes first).
+template <int AF, typename OutT, typename XIn>
+static int launch_linear_stream_t(const GemmPlan& p, const XIn* x, int64_t sxm, const uint8_t* w, int64_t ldw,
+                                  const float* ws, int64_t ws_sn, int64_t ws_sk, uint16_t* out, int64_t ldo,
+                                  int64_t M, int64_t N, int64_t K, hipStream_t stream) {
+  const int64_t kb = cdiv(K, kGroup);
+  const bool ragged = p.rows != 16 * AF || 8 % AF != 0;
+  const size_t bytes = stream_fold_bytes(kb, AF, 1, ragged ? 2 : 1);
+  if (bytes > (ragged ? kStreamFoldLdsOne : kStreamFoldLds)) return MI355X_FP8_ERR_UNSUPPORTED;
+  const dim3 grid(static_cast<unsigned>(cdiv(N, p.rows)), 1, 1);
+  const uint8_t* xq = reinterpret_cast<const uint8_t*>(x);
+  if (ragged)
+    stream_gemm_kernel<1, AF, true, true, OutT, XIn><<<grid, kStreamWaves * 64, bytes, stream>>>(
+        xq, sxm, nullptr, 0, 0, w, ldw, ws, ws_sn, ws_sk, out, ldo, M, N, K, kb, p.rows);
+  else if constexpr (8 % AF == 0)
+    stream_gemm_kernel<1, AF, true, false, OutT, XIn><<<grid, kStreamWaves * 64, bytes, stream>>>(
+        xq, sxm, nullptr, 0, 0, w, ldw, ws, ws_sn, ws_sk, out, ldo, M, N, K, kb, p.rows);
+  return hipGetLastError() == hipSuccess ? MI355X_FP8_OK : MI355X_FP8_ERR_LAUNCH;
+}
+
+template <typename OutT, typename XIn>
+static int launch_linear_stream_x(const GemmPlan& p, const XIn* x, int64_t sxm, const uint8_t* w, int64_t ldw,
+                                  const float* ws, int64_t ws_sn, int64_t ws_sk, uint16_t* out, int64_t ldo,
+                                  int64_t M, int64_t N, int64_t K, hipStream_t stream) {
+#define MI355X_LIN_ARGS p, x, sxm, w, ldw, ws, ws_sn, ws_sk, out, ldo, M, N, K, stream
+  switch (p.row_tiles) {
+    case 5: return launch_linear_stream_t<5, OutT, XIn>(MI355X_LIN_ARGS);
+    case 4: return launch_linear_stream_t<4, OutT, XIn>(MI355X_LIN_ARGS);
+    case 3: return launch_linear_stream_t<3, OutT, XIn>(MI355X_LIN_ARGS);
+    case 2: return launch_linear_stream_t<2, OutT, XIn>(MI355X_LIN_ARGS);
+    default: return launch_linear_stream_t<1, OutT, XIn>(MI355X_LIN_ARGS);
+  }
+#undef MI355X_LIN_ARGS
+}
+
+int launch_linear_stream(const GemmPlan& plan, const void* x, int x_dtype, int64_t sxm, int64_t sxk,
+                         const uint8_t* w, int64_t ldw, const float* ws, int64_t ws_sn, int64_t ws_sk, void* out,
+                         int out_dtype, int64_t ldo, int64_t M, int64_t N, int64_t K, hipStream_t stream) {
+  // One 16-token tile, and every load a whole aligned 16-byte piece: K % 16 == 0, unit
+  // column stride, 16-byte aligned rows of x and W.
+  if (plan.kernel != MI355X_FP8_CONFIG_STREAM || plan.token_tiles != 1 || M > 16 || M <= 0 || N <= 0 ||
+      plan.rows < 1 || sxk != 1 || sxm % 8 != 0 || K % 16 != 0 || ldw % 16 != 0 ||
+      reinterpret_cast<uintptr_t>(x) % 16 != 0 || reinterpret_cast<uintptr_t>(w) % 16 != 0)
+    return MI355X_FP8_ERR_UNSUPPORTED;
+#ifndef MI355X_LINEAR_ALWAYS_ONE_LAUNCH
+  // Every workgroup reads and quantizes all of x: 2 M K bytes beside its own rows x K weight
+  // bytes, and about 220 VALU instructions per K group in each of its 16 waves.  One launch
+  // pays only while x is the smaller read and a wave quantizes at most about one and a half
+  // groups.  Measured (Qwen3-4B, one launch against quantizer + GEMM): qkv and gate_up
+  // (K = 2560) 1.3-1.9 us faster at 1-16 rows; down (K = 9728) 4.3 us slower at one row,
+  // o_proj (K = 4096) 0.4 us slower.
+  if (2 * M > plan.rows || cdiv(K, kGroup) > 24) return MI355X_FP8_ERR_UNSUPPORTED;
+#endif
+  uint16_t* o = static_cast<uint16_t*>(out);
+  if (x_dtype == kBF16)
+    return out_dtype == kBF16
+               ? launch_linear_stream_x<bf16_t>(plan, static_cast<const bf16_t*>(x), sxm, w, ldw, ws, ws_sn, ws_sk, o,
+                                                ldo, M, N, K, stream)
+               : launch_linear_stream_x<f16_t>(plan, static_cast<const bf16_t*>(x), sxm, w, ldw, ws, ws_sn, ws_sk, o,
+                                               ldo, M, N, K, stream);
+  return out_dtype == kBF16
+             ? launch_linear_stream_x<bf16_t>(plan, static_cast<const f16_t*>(x), sxm, w, ldw, ws, ws_sn, ws_sk, o,
+                                              ldo, M, N, K, stream)
+             : launch_linear_stream_x<f16_t>(plan, static_cast<const f16_t*>(x), sxm, w, ldw, ws, ws_sn, ws_sk, o,
+                                             ldo, M, N, K, stream);
 }
 
 }  // namespace mi355x

@@ -42,6 +42,13 @@ int launch_block_gemm(const GemmPlan& plan, const uint8_t* q, int64_t ldq, const
                       int64_t ws_sn, int64_t ws_sk, void* out, int out_dtype, int64_t ldo,
                       int64_t M, int64_t N, int64_t K, void* workspace, hipStream_t stream);
 
+// The whole linear in one stream-kernel launch (quantization inside), for plans of the stream
+// kernel with one token tile; MI355X_FP8_ERR_UNSUPPORTED (nothing launched) when the call
+// does not fit that form.
+int launch_linear_stream(const GemmPlan& plan, const void* x, int x_dtype, int64_t sxm, int64_t sxk,
+                         const uint8_t* w, int64_t ldw, const float* ws, int64_t ws_sn, int64_t ws_sk, void* out,
+                         int out_dtype, int64_t ldo, int64_t M, int64_t N, int64_t K, hipStream_t stream);
+
 // LDS-DMA pipelined prefill kernel (tile_gemm_dma.hip) and its preconditions.
 bool tile_dma_supported(const uint8_t* q, int64_t ldq, int64_t as_sm, int64_t as_sk, const uint8_t* w,
                         int64_t ldw, int64_t M, int64_t K);

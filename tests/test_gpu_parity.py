@@ -397,6 +397,33 @@ def test_decode_linear_equals_quantizer_then_gemm(gpu, shape, rows, dtype):
     assert bitwise_equal(got2, ref), bit_mismatch_details(got2, ref)
 
 
+@pytest.mark.parametrize("shape", [ModelShape("qkv", 6144, 2560), ModelShape("gate_up", 19456, 2560),
+                                   ModelShape("k2000", 6144, 2000), ModelShape("k128", 4096, 128)],
+                         ids=lambda s: s.name)
+@pytest.mark.parametrize("rows", [1, 7, 8, 16])
+@pytest.mark.parametrize("dtype,out_dtype", [(torch.bfloat16, torch.bfloat16), (torch.float16, torch.float16),
+                                             (torch.bfloat16, torch.float16)])
+def test_one_launch_linear_equals_quantizer_then_gemm(gpu, shape, rows, dtype, out_dtype):
+    """Shapes where the decode linear runs as one launch (the stream kernel quantizing its own
+    K groups: K of at most 24 groups, K % 16 == 0, 16-byte aligned rows): the bits of the
+    activation quantizer followed by the GEMM, with the generator's special rows (zero, huge,
+    tiny, -0.0, +-448), a K tail of 80 elements, and an 8-element row padding."""
+
+    _note("one-launch linear", shape.name, rows, dtype, out_dtype)
+    x = make_activations(rows, shape.k, 23 + rows, dtype)
+    w, ws = make_weights(shape, 9)
+    xg, wg, wsg = x.to(gpu), w.to(gpu), ws.to(gpu)
+    got = fp8.mi355x_fp8_linear(xg, wg, wsg, BLOCK, output_dtype=out_dtype)
+    q, s = fp8.quantize_mi355x_fp8_activation(xg)
+    ref = torch.empty_like(got)
+    fp8.launch_block_gemm(q, wg, ref, s, wsg, config=fp8.GEMM_CONFIGS[0])
+    assert bitwise_equal(got, ref), bit_mismatch_details(got, ref)
+    padded = torch.zeros(rows, shape.k + 8, dtype=dtype, device=gpu)
+    padded[:, : shape.k] = xg
+    got2 = fp8.mi355x_fp8_linear(padded[:, : shape.k], wg, wsg, BLOCK, output_dtype=out_dtype)
+    assert bitwise_equal(got2, ref), bit_mismatch_details(got2, ref)
+
+
 @pytest.mark.parametrize("shape", [ModelShape("tail", 193, 259), ModelShape("kv", 1024, 2560),
                                    ModelShape("o", 2560, 4096)], ids=lambda s: s.name)
 @pytest.mark.parametrize("rows", [1, 7, 33, 129, 1000])
