@@ -50,7 +50,6 @@ constexpr int kDmaThreads = 256;
 #endif
 constexpr int kTileRows = 128;                          // activation rows per tile
 constexpr int kMaxBN = 160;                             // widest W tile (columns of the output tile)
-constexpr int kStageChunks = (kMaxBN + kTileRows) * 8 + 64;  // W tile, X tile, 4 x 64 scales (uint4 units)
 
 // Tile geometry for width BN (128 or 160): stage layout [W tile | X tile | scales].
 template <int BN>
@@ -60,12 +59,9 @@ struct DmaGeo {
   static constexpr int kXOff = BN * 8;                 // uint4 offset of the activation tile
   static constexpr int kScaleOff = (BN + kTileRows) * 8;
   static constexpr int kDmaPerStage = BN / 32 + 4 + 1;  // DMA instructions per wave per stage
+  static constexpr int kStageU4 = (BN + kTileRows) * 8 + 64;  // one stage, in uint4
 };
 
-__shared__ uint4 stage0[kStageChunks];
-__shared__ uint4 stage1[kStageChunks];
-__shared__ uint4 stage2[kStageChunks];
-__shared__ uint4 stage3[kStageChunks];
 
 typedef __attribute__((address_space(3))) void lds_void_t;
 
@@ -128,19 +124,19 @@ struct DmaSources {
   uint32_t use_b;     // bit i: the wave's column tile i lies in block ws_b
 };
 
-template <int S>
-__device__ __forceinline__ uint4* stage_ptr() {
-  if constexpr (S == 0) return stage0;
-  else if constexpr (S == 1) return stage1;
-  else if constexpr (S == 2) return stage2;
-  else return stage3;
+// The ring: STAGES stages of DmaGeo<BN>::kStageU4 each, in the kernel's own LDS array (sized
+// per instantiation, so the two-stage form still fits two workgroups per CU).
+template <int BN, int S>
+__device__ __forceinline__ uint4* stage_ptr(uint4* ring) {
+  return ring + S * DmaGeo<BN>::kStageU4;
 }
 
 // DMA instruction d (0 .. kDmaPerStage-1) of a stage: W rows, then X rows, then scales.
 template <int BN, int S>
-__device__ __forceinline__ void issue_one(const DmaSources& src, int64_t kb, int64_t as_sk, int wave, int d) {
+__device__ __forceinline__ void issue_one(uint4* ring, const DmaSources& src, int64_t kb, int64_t as_sk, int wave,
+                                          int d) {
   using G = DmaGeo<BN>;
-  uint4* st = stage_ptr<S>();
+  uint4* st = stage_ptr<BN, S>(ring);
   const int64_t koff = kb * kGroup;
   if (d < G::kNI) dma16(src.w + koff, src.woff[d], st + (d * 4 + wave) * 64);
   else if (d < G::kNI + 4) dma16(src.x + koff, src.xoff[d - G::kNI], st + G::kXOff + ((d - G::kNI) * 4 + wave) * 64);
@@ -148,9 +144,9 @@ __device__ __forceinline__ void issue_one(const DmaSources& src, int64_t kb, int
 }
 
 template <int BN, int S>
-__device__ __forceinline__ void issue_stage(const DmaSources& src, int64_t kb, int64_t as_sk, int wave) {
+__device__ __forceinline__ void issue_stage(uint4* ring, const DmaSources& src, int64_t kb, int64_t as_sk, int wave) {
 #pragma unroll
-  for (int d = 0; d < DmaGeo<BN>::kDmaPerStage; ++d) issue_one<BN, S>(src, kb, as_sk, wave, d);
+  for (int d = 0; d < DmaGeo<BN>::kDmaPerStage; ++d) issue_one<BN, S>(ring, src, kb, as_sk, wave, d);
 }
 
 // What the first MFMAs of a K step need, read from its stage one step early: the four
@@ -165,23 +161,23 @@ struct StepHead {
 };
 
 template <int BN, int S>
-__device__ __forceinline__ v8i read_a(int i, int wn, int r, int g) {
-  const uint4* st = stage_ptr<S>();
+__device__ __forceinline__ v8i read_a(const uint4* ring, int i, int wn, int r, int g) {
+  const uint4* st = ring + S * DmaGeo<BN>::kStageU4;
   const int row = wn * (BN / 2) + 16 * i + r;
   return pack_v8i(st[row * 8 + (g ^ (row & 7))], st[row * 8 + ((g + 4) ^ (row & 7))]);
 }
 
 template <int BN, int S>
-__device__ __forceinline__ void read_head(StepHead<BN>& h, const DmaSources& src, int64_t kb, int64_t ws_sk,
-                                          int wm, int wn, int r, int g) {
+__device__ __forceinline__ void read_head(const uint4* ring, StepHead<BN>& h, const DmaSources& src, int64_t kb,
+                                          int64_t ws_sk, int wm, int wn, int r, int g) {
   using G = DmaGeo<BN>;
-  const uint4* st = stage_ptr<S>();
+  const uint4* st = ring + S * G::kStageU4;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int row = wm * 64 + 16 * j + r;
     h.b[j] = pack_v8i(st[G::kXOff + row * 8 + (g ^ (row & 7))], st[G::kXOff + row * 8 + ((g + 4) ^ (row & 7))]);
   }
-  h.a0 = read_a<BN, S>(0, wn, r, g);
+  h.a0 = read_a<BN, S>(ring, 0, wn, r, g);
   const float* sc_lds = reinterpret_cast<const float*>(st + G::kScaleOff);
 #pragma unroll
   for (int j = 0; j < 4; ++j) h.as_v[j] = sc_lds[wm * 64 + 16 * j + r];
@@ -214,7 +210,7 @@ __device__ __forceinline__ void fold_tile(v4f (&acc)[DmaGeo<BN>::kNI][4], const 
 // The LDS reads of each part so run behind MFMAs that do not depend on them.  Every
 // output element is still folded once per K group, in K order.
 template <int BN, int STAGES, int CUR>
-__device__ __forceinline__ void k_step(v4f (&acc)[DmaGeo<BN>::kNI][4], StepHead<BN>& h, const DmaSources& src,
+__device__ __forceinline__ void k_step(uint4* ring, v4f (&acc)[DmaGeo<BN>::kNI][4], StepHead<BN>& h, const DmaSources& src,
                                        int64_t kb, int64_t KB, int64_t as_sk, int64_t ws_sk, int wave, int wm,
                                        int wn, int r, int g) {
   using G = DmaGeo<BN>;
@@ -235,11 +231,11 @@ __device__ __forceinline__ void k_step(v4f (&acc)[DmaGeo<BN>::kNI][4], StepHead<
   for (int i = 0; i < NA; ++i) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) p[i][j] = mfma_16x16x128_e4m3(a[i], h.b[j]);
-    a[i + 1] = read_a<BN, CUR>(i + 1, wn, r, g);
+    a[i + 1] = read_a<BN, CUR>(ring, i + 1, wn, r, g);
     if (i > 0) fold_tile<BN>(acc, p[i - 1], sa, sb, src.use_b, i - 1);
   }
 #pragma unroll
-  for (int i = NA + 1; i < NI; ++i) a[i] = read_a<BN, CUR>(i, wn, r, g);
+  for (int i = NA + 1; i < NI; ++i) a[i] = read_a<BN, CUR>(ring, i, wn, r, g);
   // Per weight fragment of part A: its first MFMA, the two reads of the next fragment
   // (so that the wait before this MFMA covers only the fragment it needs), then the other
   // three MFMAs, each followed by folds of the fragment before.
@@ -259,7 +255,7 @@ __device__ __forceinline__ void k_step(v4f (&acc)[DmaGeo<BN>::kNI][4], StepHead<
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
   StepHead<BN> nh;
-  read_head<BN, NXT>(nh, src, kb + 1 < KB ? kb + 1 : KB - 1, ws_sk, wm, wn, r, g);
+  read_head<BN, NXT>(ring, nh, src, kb + 1 < KB ? kb + 1 : KB - 1, ws_sk, wm, wn, r, g);
   const int64_t ahead = kb + STAGES < KB ? kb + STAGES : KB - 1;
   // The refill's DMA instructions are spread over the MFMAs of part B.
   constexpr int ND = G::kDmaPerStage, NM = 4 * NB;
@@ -268,7 +264,7 @@ __device__ __forceinline__ void k_step(v4f (&acc)[DmaGeo<BN>::kNI][4], StepHead<
     const int i = NA + t / 4, j = t % 4;
     p[i][j] = mfma_16x16x128_e4m3(a[i], h.b[j]);
 #pragma unroll
-    for (int d = t * ND / NM; d < (t + 1) * ND / NM; ++d) issue_one<BN, CUR>(src, ahead, as_sk, wave, d);
+    for (int d = t * ND / NM; d < (t + 1) * ND / NM; ++d) issue_one<BN, CUR>(ring, src, ahead, as_sk, wave, d);
     if (j == 3 && i > 0) fold_tile<BN>(acc, p[i - 1], sa, sb, src.use_b, i - 1);
     __builtin_amdgcn_sched_barrier(0);
   }
@@ -283,6 +279,7 @@ __global__ __launch_bounds__(kDmaThreads, STAGES == 2 ? 2 : 1) void tile_gemm_dm
     const uint8_t* __restrict__ w, int64_t ldw, const float* __restrict__ ws, int64_t ws_sn,
     int64_t ws_sk, uint16_t* __restrict__ out, int64_t ldo, int64_t M, int64_t N, int64_t KB,
     int64_t tiles_m, int64_t tiles_n, int vec_out) {
+  __shared__ uint4 ring[STAGES * DmaGeo<BN>::kStageU4];
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63;
@@ -338,35 +335,47 @@ __global__ __launch_bounds__(kDmaThreads, STAGES == 2 ? 2 : 1) void tile_gemm_dm
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
 
-  static_assert(STAGES >= 2 && STAGES <= 4, "stages");
-  issue_stage<BN, 0>(src, 0, as_sk, wave);
-  issue_stage<BN, 1>(src, KB > 1 ? 1 : KB - 1, as_sk, wave);
-  if constexpr (STAGES >= 3) issue_stage<BN, 2>(src, KB > 2 ? 2 : KB - 1, as_sk, wave);
-  if constexpr (STAGES >= 4) issue_stage<BN, 3>(src, KB > 3 ? 3 : KB - 1, as_sk, wave);
+  static_assert(STAGES >= 2 && STAGES <= 6, "stages");
+  issue_stage<BN, 0>(ring, src, 0, as_sk, wave);
+  issue_stage<BN, 1>(ring, src, KB > 1 ? 1 : KB - 1, as_sk, wave);
+  if constexpr (STAGES >= 3) issue_stage<BN, 2>(ring, src, KB > 2 ? 2 : KB - 1, as_sk, wave);
+  if constexpr (STAGES >= 4) issue_stage<BN, 3>(ring, src, KB > 3 ? 3 : KB - 1, as_sk, wave);
+  if constexpr (STAGES >= 5) issue_stage<BN, 4>(ring, src, KB > 4 ? 4 : KB - 1, as_sk, wave);
+  if constexpr (STAGES >= 6) issue_stage<BN, 5>(ring, src, KB > 5 ? 5 : KB - 1, as_sk, wave);
   wait_vm_lgkm0<G::kDmaPerStage * (STAGES - 1)>();
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
   StepHead<BN> h;
-  read_head<BN, 0>(h, src, 0, ws_sk, wm, wn, r, g);
+  read_head<BN, 0>(ring, h, src, 0, ws_sk, wm, wn, r, g);
   int64_t kb = 0;
+#define MI355X_KSTEP(S, KBV) k_step<BN, STAGES, S>(ring, acc, h, src, KBV, KB, as_sk, ws_sk, wave, wm, wn, r, g)
   for (; kb + STAGES <= KB; kb += STAGES) {
-    k_step<BN, STAGES, 0>(acc, h, src, kb, KB, as_sk, ws_sk, wave, wm, wn, r, g);
-    k_step<BN, STAGES, 1>(acc, h, src, kb + 1, KB, as_sk, ws_sk, wave, wm, wn, r, g);
-    if constexpr (STAGES >= 3) k_step<BN, STAGES, 2>(acc, h, src, kb + 2, KB, as_sk, ws_sk, wave, wm, wn, r, g);
-    if constexpr (STAGES >= 4) k_step<BN, STAGES, 3>(acc, h, src, kb + 3, KB, as_sk, ws_sk, wave, wm, wn, r, g);
+    MI355X_KSTEP(0, kb);
+    MI355X_KSTEP(1, kb + 1);
+    if constexpr (STAGES >= 3) MI355X_KSTEP(2, kb + 2);
+    if constexpr (STAGES >= 4) MI355X_KSTEP(3, kb + 3);
+    if constexpr (STAGES >= 5) MI355X_KSTEP(4, kb + 4);
+    if constexpr (STAGES >= 6) MI355X_KSTEP(5, kb + 5);
   }
   // The last KB % STAGES groups.
-  if (kb < KB) k_step<BN, STAGES, 0>(acc, h, src, kb, KB, as_sk, ws_sk, wave, wm, wn, r, g);
+  if (kb < KB) MI355X_KSTEP(0, kb);
   if constexpr (STAGES >= 3)
-    if (kb + 1 < KB) k_step<BN, STAGES, 1>(acc, h, src, kb + 1, KB, as_sk, ws_sk, wave, wm, wn, r, g);
+    if (kb + 1 < KB) MI355X_KSTEP(1, kb + 1);
   if constexpr (STAGES >= 4)
-    if (kb + 2 < KB) k_step<BN, STAGES, 2>(acc, h, src, kb + 2, KB, as_sk, ws_sk, wave, wm, wn, r, g);
+    if (kb + 2 < KB) MI355X_KSTEP(2, kb + 2);
+  if constexpr (STAGES >= 5)
+    if (kb + 3 < KB) MI355X_KSTEP(3, kb + 3);
+  if constexpr (STAGES >= 6)
+    if (kb + 4 < KB) MI355X_KSTEP(4, kb + 4);
+#undef MI355X_KSTEP
   wait_vm_lgkm0<0>();  // no DMA may still target LDS when the workgroup ends
 
   if (vec_out == 2) {
     // Through LDS (staged_index, fp8_common.h): tile rows 0-63 in stage0, 64-127 in stage1.
-    static_assert(64 * staged_pitch<BN>() * 2 <= kStageChunks * 16, "staged rows fit a stage");
+    static_assert(64 * staged_pitch<BN>() * 2 <= DmaGeo<BN>::kStageU4 * 16, "staged rows fit a stage");
     __syncthreads();  // every wave is done with the ring
+    uint4* const stage0 = stage_ptr<BN, 0>(ring);
+    uint4* const stage1 = stage_ptr<BN, 1>(ring);
     uint16_t* reg = reinterpret_cast<uint16_t*>(wm == 0 ? stage0 : stage1);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
