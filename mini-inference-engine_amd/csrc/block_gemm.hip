@@ -532,7 +532,7 @@ int plan_gemm(int64_t M, int64_t N, int64_t K, int config, GemmPlan* plan) {
   // qkv 32 -> 24 measured 6.84 -> 6.93 us and keeps 32.  At least kStreamMinRows rows per
   // workgroup, so that narrow weights do not spread over workgroups for a few rows each.
   {
-    const int64_t slices = cdiv(M, 16 * plan->token_tiles);
+    const int64_t slices = M > 0 ? cdiv(M, 16 * plan->token_tiles) : 1;
     const int64_t cus = device_cus(), share = cus / slices > 1 ? cus / slices : 1;
     const int64_t rows = cdiv(N, share) > kStreamMinRows ? cdiv(N, share) : kStreamMinRows;
     const int64_t af = cdiv(rows, 16);
