@@ -15,13 +15,15 @@
 // row halves.
 //
 // Kernels here:
-//   stream_gemm_kernel  decode-sized M (16 or 32 rows per slice).  HBM-bound weight
-//   (+ rounds variant)  streaming: each workgroup owns 16 or 32 W rows over the whole of
-//                       K, W goes global -> registers (read once per slice, one K group in
-//                       flight per wave), the small activation matrix is served from L2;
-//                       the K groups' MFMA partials meet in LDS and are folded in K order,
-//                       so the bits equal the prefill kernels'.  No workspace, no
-//                       cross-workgroup synchronisation.
+//   stream_gemm_kernel  decode-sized M (16 or 32 tokens per slice).  HBM-bound weight
+//   (+ rounds variant)  streaming: each workgroup owns up to 80 W rows over the whole of K
+//                       (the same number on every CU where that fits), W goes global ->
+//                       registers (read once per slice, one or two K groups in flight per
+//                       wave), the small activation matrix is served from L2 (or quantized
+//                       in the kernel, for the one-launch linear); the K groups' MFMA
+//                       partials meet in LDS and are folded in K order, so the bits equal
+//                       the prefill kernels'.  No workspace, no cross-workgroup
+//                       synchronisation.
 //   tile_gemm_kernel    prefill-sized M.  MFMA-bound: 128x128 output tile per 256-thread
 //                       workgroup, 2x2 waves of 64x64, K groups staged global -> registers
 //                       -> LDS with double buffering and an XOR-swizzled (conflict-free)
@@ -38,15 +40,15 @@ constexpr int kThreads = 256;  // tile kernel
 // ------------------------------------------------------------------------------------
 // Stream kernel (decode M)
 // ------------------------------------------------------------------------------------
-// One workgroup owns 16*AF consecutive W rows and reads them over the whole of K exactly
-// once.  Its 16 waves take K groups round-robin (wave w: w, w + 16, ...) with the next one
+// One workgroup owns up to 16*AF consecutive W rows and reads them over the whole of K
+// exactly once.  Its 16 waves take K groups round-robin (wave w: w, w + 16, ...) with the next one
 // or two groups' loads in flight, and compute each group's MFMA partial; the partials then
 // meet in LDS, where one thread per output element folds them in K order (below).  16
 // waves per workgroup measured best on the Qwen3-4B shapes.
 constexpr int kStreamWaves = 16;
 // One-round partial buffer limit: two workgroups of 1024 threads share a CU's 160 KiB.
 constexpr size_t kStreamFoldLds = 80 * 1024;
-// With at most one workgroup per CU (the five-tile form) the buffer may take most of the LDS.
+// With at most one workgroup per CU (the ragged row counts) the buffer may take most of the LDS.
 constexpr size_t kStreamFoldLdsOne = 144 * 1024;
 constexpr int64_t kStreamMinRows = 8;
 
