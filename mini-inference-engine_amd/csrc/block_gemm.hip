@@ -222,10 +222,11 @@ __global__ __launch_bounds__(kStreamWaves * 64) void stream_gemm_kernel(
   const int64_t wave_u = __builtin_amdgcn_readfirstlane(wave);
 
   // Operands of one K group in registers.  Waves keep two groups of loads in flight when
-  // the workgroup holds one 16 x 16 tile (measured on the Qwen3-4B shapes at M = 8: qkv
-  // 7.8 -> 7.4 us, o_proj 6.9 -> 6.3 us), one otherwise (gate_up's two row tiles measured
-  // 15.2 -> 16.5 us with two; unaligned shapes assemble their loads from bytes and need
-  // the registers).
+  // the workgroup holds up to three 16-row tiles of one token tile (two when quantizing),
+  // one otherwise: measured at M = 8, o_proj 6.9 -> 6.3 us (one tile), qkv 6.83 -> 6.44 us
+  // (two tiles), an 11008-row weight 12.35 -> 11.65 us (three); with five tiles the
+  // registers spill (gate_up 12.8 -> 17.4 us), and unaligned shapes assemble their loads
+  // from bytes and need the registers.
   struct Operands {
     v8i a[AF], b[NT];
     float asv[NT], wsv[kSB];
@@ -314,7 +315,7 @@ __global__ __launch_bounds__(kStreamWaves * 64) void stream_gemm_kernel(
         for (int j = 0; j < NT; ++j) scl[(kb * kSB + b) * kTok + 16 * j + r] = sc[b][j];
     }
   };
-  constexpr int kDepth = ALIGNED && AF == 1 && NT == 1 ? 2 : 1;
+  constexpr int kDepth = ALIGNED && NT == 1 && AF <= (kQuant ? 2 : 3) ? 2 : 1;
   constexpr int64_t kStep = static_cast<int64_t>(kStreamWaves) * kDepth;
   Operands ops[kDepth];
 #pragma unroll
