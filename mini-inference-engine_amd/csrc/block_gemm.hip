@@ -185,7 +185,7 @@ __global__ __launch_bounds__(kStreamWaves * 64) void stream_rounds_kernel(
 // a workgroup owns exactly 16 AF rows with 8 % AF == 0, inside one block.
 extern __shared__ float4 stream_fold_lds[];
 
-template <int NT, int AF, bool ALIGNED, bool RAGGED, typename OutT, typename XIn = uint8_t>
+template <int NT, int AF, bool ALIGNED, bool RAGGED, typename OutT, typename XIn = uint8_t, int QT = 16>
 __global__ __launch_bounds__(kStreamWaves * 64) void stream_gemm_kernel(
     const uint8_t* __restrict__ q, int64_t ldq, const float* __restrict__ as, int64_t as_sm,
     int64_t as_sk, const uint8_t* __restrict__ w, int64_t ldw, const float* __restrict__ ws,
@@ -200,6 +200,16 @@ __global__ __launch_bounds__(kStreamWaves * 64) void stream_gemm_kernel(
   constexpr bool kQuant = !std::is_same<XIn, uint8_t>::value;
   using XT = typename std::conditional<kQuant, XIn, bf16_t>::type;  // element type when quantizing
   static_assert(!kQuant || (ALIGNED && NT == 1), "in-kernel quantization: aligned, one token tile");
+  // QT: tokens one quantization pass covers (at least the slice's rows).  16: each lane
+  // quantizes 32 elements of its own MFMA operand row (token r = lane % 16), so with fewer
+  // tokens the lanes of the missing ones idle.  8, 4 or 2: the 64 lanes share the QT
+  // tokens' groups, kLPT consecutive lanes per token and 2 QT consecutive elements each,
+  // and the codes and scales then move to the MFMA operand layout by ds_bpermute.  Same
+  // amax (a maximum: order-free), scale and per-element division, so the same bits.
+  static_assert(QT == 16 || QT == 8 || QT == 4 || QT == 2, "tokens per quantization pass");
+  constexpr bool kDense = kQuant && QT < 16;
+  constexpr int kLPT = 64 / QT;  // lanes per token (dense pass)
+  constexpr int kE = 128 / kLPT; // elements per lane (dense pass)
   constexpr int kRows = 16 * AF;
   constexpr int kTok = 16 * NT;
   constexpr int kSB = RAGGED ? 2 : 1;
@@ -230,10 +240,41 @@ __global__ __launch_bounds__(kStreamWaves * 64) void stream_gemm_kernel(
   struct Operands {
     v8i a[AF], b[NT];
     float asv[NT], wsv[kSB];
-    uint4 xr[kQuant ? 4 : 1];  // unquantized activations: elements 16 g .. +15 and 64 + 16 g .. +15
+    // Unquantized activations: elements 16 g .. +15 and 64 + 16 g .. +15 of token r (QT = 16),
+    // or the kE elements of this lane's share (dense pass), as raw 16-bit pairs.
+    uint32_t xr[kQuant ? (kDense ? kE / 2 : 16) : 1];
   };
   auto load = [&](Operands& o, int64_t kb) {
     const int64_t k_lo = kb * kGroup + 16 * g;
+    // Unquantized activations first: loads complete in issue order, so the wait for them
+    // (before the group's quantization) then leaves this group's weight loads in flight, and
+    // the quantization overlaps them (qkv and gate_up linears 0.2-0.4 us faster at 1-8 rows).
+    if constexpr (kDense) {
+      // Token lane / kLPT, elements kb * 128 + (lane % kLPT) kE .. + kE - 1 (K % 16 == 0 and
+      // kE divides 16, so a share is either whole or past K).
+      const int t = lane / kLPT;
+      const int64_t k = kb * kGroup + (lane % kLPT) * kE;
+      const XT* xp = reinterpret_cast<const XT*>(q) + (m_base + t) * ldq + k;
+      const bool ok = t < m_rows && k < K;
+#pragma unroll
+      for (int c = 0; c < kE / 8; ++c) {
+        const uint4 v = ok ? reinterpret_cast<const uint4*>(xp)[c] : make_uint4(0u, 0u, 0u, 0u);
+        o.xr[4 * c] = v.x; o.xr[4 * c + 1] = v.y; o.xr[4 * c + 2] = v.z; o.xr[4 * c + 3] = v.w;
+      }
+      if constexpr (kE == 4) {
+        const uint2 v = ok ? *reinterpret_cast<const uint2*>(xp) : make_uint2(0u, 0u);
+        o.xr[0] = v.x; o.xr[1] = v.y;
+      }
+    } else if constexpr (kQuant) {
+      const int64_t m = m_base + r;
+      const XT* xrow = reinterpret_cast<const XT*>(q) + m * ldq;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const int64_t k = k_lo + 64 * (c >> 1) + 8 * (c & 1);
+        const uint4 v = (r < m_rows && k < K) ? *reinterpret_cast<const uint4*>(xrow + k) : make_uint4(0u, 0u, 0u, 0u);
+        o.xr[4 * c] = v.x; o.xr[4 * c + 1] = v.y; o.xr[4 * c + 2] = v.z; o.xr[4 * c + 3] = v.w;
+      }
+    }
 #pragma unroll
     for (int i = 0; i < AF; ++i) {
       const int64_t row = n0 + 16 * i + r;
@@ -242,15 +283,7 @@ __global__ __launch_bounds__(kStreamWaves * 64) void stream_gemm_kernel(
     }
     o.wsv[0] = ws[nb0 * ws_sn + kb * ws_sk];
     if constexpr (RAGGED) o.wsv[kSB - 1] = ws[nb1 * ws_sn + kb * ws_sk];
-    if constexpr (kQuant) {
-      const int64_t m = m_base + r;
-      const XT* xrow = reinterpret_cast<const XT*>(q) + m * ldq;
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const int64_t k = k_lo + 64 * (c >> 1) + 8 * (c & 1);
-        o.xr[c] = (r < m_rows && k < K) ? *reinterpret_cast<const uint4*>(xrow + k) : make_uint4(0u, 0u, 0u, 0u);
-      }
-    } else {
+    if constexpr (!kQuant) {
 #pragma unroll
       for (int j = 0; j < NT; ++j) {
         const int64_t tok = 16 * j + r;
@@ -263,28 +296,51 @@ __global__ __launch_bounds__(kStreamWaves * 64) void stream_gemm_kernel(
   // The 1x128 quantizer on the lane's 32 elements of its token's K group; the four lanes of a
   // token (g = 0..3) hold the whole group, so the amax takes two cross-lane steps.
   auto quantize = [&](Operands& o) {
-    float t[32];
+    constexpr int kN = kDense ? kE : 32;  // elements this lane quantizes
+    float t[kN];
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const uint32_t wv[4] = {o.xr[c].x, o.xr[c].y, o.xr[c].z, o.xr[c].w};
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        t[8 * c + 2 * e] = to_f32(XT{static_cast<uint16_t>(wv[e] & 0xffffu)});
-        t[8 * c + 2 * e + 1] = to_f32(XT{static_cast<uint16_t>(wv[e] >> 16)});
-      }
+    for (int e = 0; e < kN / 2; ++e) {
+      t[2 * e] = to_f32(XT{static_cast<uint16_t>(o.xr[e] & 0xffffu)});
+      t[2 * e + 1] = to_f32(XT{static_cast<uint16_t>(o.xr[e] >> 16)});
     }
     float amax = 0.0f;
 #pragma unroll
-    for (int e = 0; e < 32; ++e) amax = fmaxf(amax, fabsf(t[e]));
-    amax = fmaxf(amax, __shfl_xor(amax, 16));
-    amax = fmaxf(amax, __shfl_xor(amax, 32));
+    for (int e = 0; e < kN; ++e) amax = fmaxf(amax, fabsf(t[e]));
+    if constexpr (kDense) {
+#pragma unroll
+      for (int off = 1; off < kLPT; off <<= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
+    } else {
+      // The four lanes of a token (g = 0..3) hold the whole group.
+      amax = fmaxf(amax, __shfl_xor(amax, 16));
+      amax = fmaxf(amax, __shfl_xor(amax, 32));
+    }
     const float scale = amax / 448.0f;
     const float den = scale > 1e-12f ? scale : 1e-12f;
-    uint32_t packed[8];
-    quant_codes<32>(t, den, packed);
-    o.b[0] = pack_v8i(make_uint4(packed[0], packed[1], packed[2], packed[3]),
-                      make_uint4(packed[4], packed[5], packed[6], packed[7]));
-    o.asv[0] = scale;
+    uint32_t packed[kN / 4];
+    quant_codes<kN>(t, den, packed);
+    if constexpr (kDense) {
+      // Operand lane (r, g) takes token r's code words 4 g .. 4 g + 3 and 16 + 4 g .. +3; word d
+      // of token r sits in lane r kLPT + d / (kE / 4), slot d % (kE / 4), which is j % (kE / 4)
+      // for both ranges (kE / 4 divides 4).
+      constexpr int kW = kE / 4;
+      const int src0 = r * kLPT;
+      v8i b;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        b[j] = __builtin_amdgcn_ds_bpermute(4 * (src0 + (4 * g + j) / kW), static_cast<int>(packed[j % kW]));
+        b[4 + j] = __builtin_amdgcn_ds_bpermute(4 * (src0 + (16 + 4 * g + j) / kW), static_cast<int>(packed[j % kW]));
+      }
+      const float sc = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(4 * src0, __builtin_bit_cast(int, scale)));
+      const bool live = r < QT;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) b[j] = live ? b[j] : 0;
+      o.b[0] = b;
+      o.asv[0] = live ? sc : 0.0f;
+    } else {
+      o.b[0] = pack_v8i(make_uint4(packed[0], packed[1], packed[2], packed[3]),
+                        make_uint4(packed[4], packed[5], packed[6], packed[7]));
+      o.asv[0] = scale;
+    }
   };
   // MFMA partials of group kb and their publication; `refill` loads group kb_next into the
   // registers just consumed (issued before the LDS writes, so it overlaps them).
@@ -757,8 +813,8 @@ int launch_block_gemm(const GemmPlan& plan, const uint8_t* q, int64_t ldq, const
 // The whole linear in one launch at decode sizes: the stream kernel quantizing its own K
 // groups (XIn = bf16_t / f16_t).  Returns MI355X_FP8_ERR_UNSUPPORTED, having launched
 // nothing, when the call does not fit that form (then the caller quantizes first).
-template <int AF, typename OutT, typename XIn>
-static int launch_linear_stream_t(const GemmPlan& p, const XIn* x, int64_t sxm, const uint8_t* w, int64_t ldw,
+template <int AF, typename OutT, typename XIn, int QT>
+static int launch_linear_stream_q(const GemmPlan& p, const XIn* x, int64_t sxm, const uint8_t* w, int64_t ldw,
                                   const float* ws, int64_t ws_sn, int64_t ws_sk, uint16_t* out, int64_t ldo,
                                   int64_t M, int64_t N, int64_t K, hipStream_t stream) {
   const int64_t kb = cdiv(K, kGroup);
@@ -768,12 +824,23 @@ static int launch_linear_stream_t(const GemmPlan& p, const XIn* x, int64_t sxm, 
   const dim3 grid(static_cast<unsigned>(cdiv(N, p.rows)), 1, 1);
   const uint8_t* xq = reinterpret_cast<const uint8_t*>(x);
   if (ragged)
-    stream_gemm_kernel<1, AF, true, true, OutT, XIn><<<grid, kStreamWaves * 64, bytes, stream>>>(
+    stream_gemm_kernel<1, AF, true, true, OutT, XIn, QT><<<grid, kStreamWaves * 64, bytes, stream>>>(
         xq, sxm, nullptr, 0, 0, w, ldw, ws, ws_sn, ws_sk, out, ldo, M, N, K, kb, p.rows);
   else if constexpr (8 % AF == 0)
-    stream_gemm_kernel<1, AF, true, false, OutT, XIn><<<grid, kStreamWaves * 64, bytes, stream>>>(
+    stream_gemm_kernel<1, AF, true, false, OutT, XIn, QT><<<grid, kStreamWaves * 64, bytes, stream>>>(
         xq, sxm, nullptr, 0, 0, w, ldw, ws, ws_sn, ws_sk, out, ldo, M, N, K, kb, p.rows);
   return hipGetLastError() == hipSuccess ? MI355X_FP8_OK : MI355X_FP8_ERR_LAUNCH;
+}
+
+// Tokens per quantization pass: the fewest of 2, 4, 8 and 16 that hold the rows.
+template <int AF, typename OutT, typename XIn>
+static int launch_linear_stream_t(const GemmPlan& p, const XIn* x, int64_t sxm, const uint8_t* w, int64_t ldw,
+                                  const float* ws, int64_t ws_sn, int64_t ws_sk, uint16_t* out, int64_t ldo,
+                                  int64_t M, int64_t N, int64_t K, hipStream_t stream) {
+  if (M <= 2) return launch_linear_stream_q<AF, OutT, XIn, 2>(p, x, sxm, w, ldw, ws, ws_sn, ws_sk, out, ldo, M, N, K, stream);
+  if (M <= 4) return launch_linear_stream_q<AF, OutT, XIn, 4>(p, x, sxm, w, ldw, ws, ws_sn, ws_sk, out, ldo, M, N, K, stream);
+  if (M <= 8) return launch_linear_stream_q<AF, OutT, XIn, 8>(p, x, sxm, w, ldw, ws, ws_sn, ws_sk, out, ldo, M, N, K, stream);
+  return launch_linear_stream_q<AF, OutT, XIn, 16>(p, x, sxm, w, ldw, ws, ws_sn, ws_sk, out, ldo, M, N, K, stream);
 }
 
 template <typename OutT, typename XIn>
@@ -801,13 +868,17 @@ int launch_linear_stream(const GemmPlan& plan, const void* x, int x_dtype, int64
       reinterpret_cast<uintptr_t>(x) % 16 != 0 || reinterpret_cast<uintptr_t>(w) % 16 != 0)
     return MI355X_FP8_ERR_UNSUPPORTED;
 #ifndef MI355X_LINEAR_ALWAYS_ONE_LAUNCH
-  // Every workgroup reads and quantizes all of x: 2 M K bytes beside its own rows x K weight
-  // bytes, and about 220 VALU instructions per K group in each of its 16 waves.  One launch
-  // pays only while x is the smaller read and a wave quantizes at most about one and a half
-  // groups.  Measured (Qwen3-4B, one launch against quantizer + GEMM): qkv and gate_up
-  // (K = 2560) 1.3-1.9 us faster at 1-16 rows; down (K = 9728) 4.3 us slower at one row,
-  // o_proj (K = 4096) 0.4 us slower.
-  if (2 * M > plan.rows || cdiv(K, kGroup) > 24) return MI355X_FP8_ERR_UNSUPPORTED;
+  // Every workgroup reads and quantizes all of x, about 7 VALU instructions per element of
+  // x: the quantization pays only while it hides behind the workgroup's own weight loads.
+  // Up to 8 rows (the lane-dense quantization passes) that holds for every Qwen3-4B
+  // projection, K = 9728 included.  Measured, one launch against quantizer + GEMM: at 8 rows
+  // o_proj 8.77 -> 7.14 us, down 12.6 -> 11.8 us; at 1 row o_proj 7.95 -> 6.49 us, down
+  // 11.0 -> 10.0 us.  At 9-16 rows the 16-token pass quantizes twice the elements per lane
+  // and one launch pays only while x is the smaller read and a wave quantizes at most about
+  // one and a half groups (qkv and gate_up, K = 2560: 1.3-1.9 us faster; down at 16 rows
+  // 14.6 -> 18.5 us, o_proj 9.4 -> 9.9 us).
+  const int64_t kgroups = cdiv(K, kGroup);
+  if (M <= 8 ? kgroups > 80 : (2 * M > plan.rows || kgroups > 24)) return MI355X_FP8_ERR_UNSUPPORTED;
 #endif
   uint16_t* o = static_cast<uint16_t*>(out);
   if (x_dtype == kBF16)

@@ -398,16 +398,19 @@ def test_decode_linear_equals_quantizer_then_gemm(gpu, shape, rows, dtype):
 
 
 @pytest.mark.parametrize("shape", [ModelShape("qkv", 6144, 2560), ModelShape("gate_up", 19456, 2560),
+                                   ModelShape("o_proj", 2560, 4096), ModelShape("down", 2560, 9728),
                                    ModelShape("k2000", 6144, 2000), ModelShape("k128", 4096, 128)],
                          ids=lambda s: s.name)
-@pytest.mark.parametrize("rows", [1, 7, 8, 16])
+@pytest.mark.parametrize("rows", [1, 2, 3, 4, 5, 7, 8, 9, 16])
 @pytest.mark.parametrize("dtype,out_dtype", [(torch.bfloat16, torch.bfloat16), (torch.float16, torch.float16),
                                              (torch.bfloat16, torch.float16)])
 def test_one_launch_linear_equals_quantizer_then_gemm(gpu, shape, rows, dtype, out_dtype):
     """Shapes where the decode linear runs as one launch (the stream kernel quantizing its own
-    K groups: K of at most 24 groups, K % 16 == 0, 16-byte aligned rows): the bits of the
-    activation quantizer followed by the GEMM, with the generator's special rows (zero, huge,
-    tiny, -0.0, +-448), a K tail of 80 elements, and an 8-element row padding."""
+    K groups: up to 8 rows for K of up to 80 groups, or K of at most 24 groups; K % 16 == 0,
+    16-byte aligned rows), through each quantization pass (2, 4, 8 and 16 tokens): the bits
+    of the activation quantizer followed by the GEMM, with the generator's special rows
+    (zero, huge, tiny, -0.0, +-448), a K tail of 80 elements, and an 8-element row padding.
+    (Shapes outside the one-launch rule take the two launches and compare trivially.)"""
 
     _note("one-launch linear", shape.name, rows, dtype, out_dtype)
     x = make_activations(rows, shape.k, 23 + rows, dtype)
