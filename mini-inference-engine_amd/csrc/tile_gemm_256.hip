@@ -6,7 +6,7 @@
 // acc = fma(partial, a_s * w_s, acc), K groups in increasing order.  The tile shape does
 // not enter the arithmetic, so every tile width gives the same bits as the other kernels.
 //
-// Why 256 rows: a CU sustains about 40 B/clk from L2 and 128 B/clk from LDS.  A per-CU
+// Why 256 rows: a CU sustains about 40 B/clk from L2 (its LDS reads about 256 B/clk).  A per-CU
 // output tile of BM x BN needs (BM + BN) * 128 bytes of operands per K group for
 // 2 * BM * BN * 128 flops; at 256x256 that is 22 B/clk at 70 % of the fp8 MFMA peak,
 // where 128x128 would need 44 B/clk, more than L2 delivers.
