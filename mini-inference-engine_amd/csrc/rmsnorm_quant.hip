@@ -6,7 +6,10 @@
 // (engine/kernels/sm89_fp8.py:304-332) applied to the result:
 //   x    = bf16(x + residual)           residual variant (fp32 add, one rounding; also stored)
 //   ss   = sum of rounded squares x*x  in PyTorch's reduction order (below)
-//   var  = ss * fl(1 / K)              a separate rounding (no fused multiply-add)
+//   var  = ss * fl(1 / K)              a separate rounding (no fused multiply-add: __fmul_rn and
+//                                      __fadd_rn are plain operators in HIP, so the library is
+//                                      built with -ffp-contract=off; fused, var + eps came out
+//                                      one rounding short and moved y by one ulp near ties)
 //   inv  = 1 / sqrt(var + eps)         here computed in double and rounded once to fp32
 //   y    = bf16(w * bf16(x * inv))
 //   q, s = the quantizer of y

@@ -21,8 +21,11 @@ HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 FLAGS = (
     "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-shared", "-Wall",
-    # Keep fp32 math as separate IEEE operations: no fast-math, correctly rounded division.
-    "-fno-fast-math",
+    # Keep fp32 math as separate IEEE operations: no fast-math, correctly rounded division,
+    # and no contraction of a multiply and an add into one fma (hipcc contracts by default;
+    # the RMSNorm's var = ss * (1 / K) and var + eps are two roundings, as in the reference).
+    # Every fma the kernels mean is written as one (__builtin_fmaf).
+    "-fno-fast-math", "-ffp-contract=off",
     # No packed-fp32 VALU instructions (v_pk_*_f32) anywhere in the library.
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     # MFMA results in ordinary VGPRs: the per-K-group fold (acc = fma(partial, scale, acc))

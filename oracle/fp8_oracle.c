@@ -262,35 +262,62 @@ int64_t orc_rmsnorm_block_width(int64_t rows, int64_t n_cols) {
  *         reference uses libdevice's approximate rsqrt here)
  *   y   = bf16(w * bf16(x * inv))
  * x and residual rows are `ld` elements apart; y and summed are dense. */
+/* The row's sum of squares in the reference's order (fused.py:95-115, the tree of
+ * fused.py:61-75): part[] holds bw floats of scratch. */
+static float orc_rms_sumsq(const float* xs, int64_t n_cols, int64_t bw, float* part) {
+  const int64_t nvec = n_cols / 4;
+  for (int64_t t = 0; t < bw; ++t) {
+    float a[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int64_t v = t; v < nvec; v += bw)
+      for (int q = 0; q < 4; ++q) {
+        float sq = xs[4 * v + q] * xs[4 * v + q];
+        a[q] = a[q] + sq;
+      }
+    part[t] = ((a[0] + a[1]) + a[2]) + a[3];
+  }
+  for (int64_t h = bw / 2; h >= 1; h /= 2)
+    for (int64_t t = 0; t < h; ++t) part[t] = part[t] + part[t + h];
+  return part[0];
+}
+
+/* Row r's x (bf16(x + residual) with a residual, whose bits go to summed when non-null). */
+static void orc_rms_row(const uint16_t* x, const uint16_t* residual, int64_t ld, int64_t r, int64_t n_cols,
+                        float* xs, uint16_t* summed) {
+  for (int64_t c = 0; c < n_cols; ++c) {
+    float v = orc_bf16_to_f32(x[r * ld + c]);
+    if (residual) {
+      uint16_t sb = orc_f32_to_bf16(v + orc_bf16_to_f32(residual[r * ld + c]));
+      if (summed) summed[r * n_cols + c] = sb;
+      v = orc_bf16_to_f32(sb);
+    }
+    xs[c] = v;
+  }
+}
+
+/* The sums of squares orc_rmsnorm forms, one per row (exposed so that tests can pin the
+ * summation order itself). */
+void orc_rmsnorm_sumsq(const uint16_t* x, const uint16_t* residual, int64_t ld, int64_t rows, int64_t n_cols,
+                       float* out) {
+  const int64_t bw = orc_rmsnorm_block_width(rows, n_cols);
+  float* part = (float*)malloc((size_t)bw * sizeof(float));
+  float* xs = (float*)malloc((size_t)n_cols * sizeof(float));
+  for (int64_t r = 0; r < rows; ++r) {
+    orc_rms_row(x, residual, ld, r, n_cols, xs, NULL);
+    out[r] = orc_rms_sumsq(xs, n_cols, bw, part);
+  }
+  free(part);
+  free(xs);
+}
+
 void orc_rmsnorm(const uint16_t* x, const uint16_t* residual, int64_t ld, const uint16_t* w, int64_t rows,
                  int64_t n_cols, float eps, uint16_t* y, uint16_t* summed) {
   const int64_t bw = orc_rmsnorm_block_width(rows, n_cols);
-  const int64_t nvec = n_cols / 4;
   const float inv_k = 1.0f / (float)n_cols;
   float* part = (float*)malloc((size_t)bw * sizeof(float));
   float* xs = (float*)malloc((size_t)n_cols * sizeof(float));
   for (int64_t r = 0; r < rows; ++r) {
-    for (int64_t c = 0; c < n_cols; ++c) {
-      float v = orc_bf16_to_f32(x[r * ld + c]);
-      if (residual) {
-        uint16_t sb = orc_f32_to_bf16(v + orc_bf16_to_f32(residual[r * ld + c]));
-        summed[r * n_cols + c] = sb;
-        v = orc_bf16_to_f32(sb);
-      }
-      xs[c] = v;
-    }
-    for (int64_t t = 0; t < bw; ++t) {
-      float a[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-      for (int64_t v = t; v < nvec; v += bw)
-        for (int q = 0; q < 4; ++q) {
-          float sq = xs[4 * v + q] * xs[4 * v + q];
-          a[q] = a[q] + sq;
-        }
-      part[t] = ((a[0] + a[1]) + a[2]) + a[3];
-    }
-    for (int64_t h = bw / 2; h >= 1; h /= 2)
-      for (int64_t t = 0; t < h; ++t) part[t] = part[t] + part[t + h];
-    float var = part[0] * inv_k;
+    orc_rms_row(x, residual, ld, r, n_cols, xs, summed);
+    float var = orc_rms_sumsq(xs, n_cols, bw, part) * inv_k;
     float inv = (float)(1.0 / sqrt((double)(var + eps)));
     for (int64_t c = 0; c < n_cols; ++c) {
       float normed = orc_bf16_to_f32(orc_f32_to_bf16(xs[c] * inv));

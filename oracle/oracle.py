@@ -57,6 +57,7 @@ def lib():
         handle.orc_rmsnorm_block_width.argtypes = [_i64, _i64]
         handle.orc_rmsnorm_block_width.restype = _i64
         handle.orc_rmsnorm.argtypes = [_ptr, _ptr, _i64, _ptr, _i64, _i64, ctypes.c_float, _ptr, _ptr]
+        handle.orc_rmsnorm_sumsq.argtypes = [_ptr, _ptr, _i64, _i64, _i64, _ptr]
         _lib = handle
     return _lib
 
@@ -180,6 +181,18 @@ def rmsnorm(x_bits: np.ndarray, w_bits: np.ndarray, eps: float,
     lib().orc_rmsnorm(_p(x), None if r is None else _p(r), n_cols, _p(w), rows, n_cols, float(eps), _p(y),
                       None if summed is None else _p(summed))
     return y, summed
+
+
+def rmsnorm_sumsq(x_bits: np.ndarray, residual_bits: np.ndarray | None = None) -> np.ndarray:
+    """Per-row fp32 sum of squares that ``rmsnorm`` forms (same order, same rows in a batch
+    of this many rows), for tests that pin the summation order."""
+
+    x = np.ascontiguousarray(x_bits, dtype=np.uint16)
+    rows, n_cols = x.shape
+    r = None if residual_bits is None else np.ascontiguousarray(residual_bits, dtype=np.uint16)
+    out = np.empty(rows, dtype=np.float32)
+    lib().orc_rmsnorm_sumsq(_p(x), None if r is None else _p(r), n_cols, rows, n_cols, _p(out))
+    return out
 
 
 def max_threads() -> int:

@@ -9,7 +9,7 @@ import pytest
 import torch
 
 import oracle
-from _helpers import assert_close_rows, bits16, codes, oracle_linear
+from _helpers import assert_close_rows, bits16, codes, crafted_sumsq_rows, oracle_linear, sumsq_eps_sweep
 from minillm_amd import merged_projections as mp
 from minillm_amd import mi355x_fp8 as fp8
 from minillm_amd.validation import (
@@ -170,6 +170,30 @@ def test_rmsnorm_quant_matches_oracle(gpu, rows, width, with_residual):
     outs2 = fp8.rmsnorm_quant_mi355x_fp8(x.to(gpu), w.to(gpu), 1e-6, None if r is None else r.to(gpu))
     assert bitwise_equal(outs2[0], q)
     assert np.array_equal(outs2[1].cpu().numpy().view(np.uint32), s.cpu().numpy().view(np.uint32))
+
+
+@pytest.mark.parametrize("rows,width", [(1, 2560), (2, 2560), (16, 2560), (3, 1024), (1, 128)])
+def test_rmsnorm_summation_order_on_crafted_rows(gpu, rows, width):
+    """The kernel's row sum follows the reference's order (fused.py:61-75, 95-115): on rows
+    whose fp32 sum of squares that order fixes in closed form, and other orders change
+    (_helpers.crafted_sumsq_rows), over an eps sweep at which those sums give different y
+    (_helpers.sumsq_eps_sweep), y equals the oracle's bit for bit, and its 4096 element
+    equals the value the closed-form sum gives."""
+
+    _note("rmsnorm order", rows, width)
+    bw = oracle.rmsnorm_block_width(rows, width)
+    w = torch.ones(width, dtype=torch.bfloat16)
+    for name, x, expect in crafted_sumsq_rows(rows, width, bw):
+        xg = x.to(gpu)
+        for eps in sumsq_eps_sweep(width, expect, name):
+            y = fp8.rmsnorm_quant_mi355x_fp8(xg, w.to(gpu), eps, scale_layout="row", return_intermediate=True)[0]
+            y_ref, _ = oracle.rmsnorm(bits16(x), bits16(w), eps)
+            got = bits16(y)
+            assert np.array_equal(got, y_ref), (name, eps)
+            var = np.float32(np.float32(expect) * np.float32(np.float32(1.0) / np.float32(width)))
+            inv = np.float32(1.0 / np.sqrt(np.float64(np.float32(var + np.float32(eps)))))
+            y0 = torch.tensor(float(np.float32(np.float32(4096.0) * inv))).to(torch.bfloat16)
+            assert int(got[0, 0]) == int(bits16(y0.reshape(1))[0]), (name, eps)
 
 
 def test_rmsnorm_linear_equals_unfused(gpu):

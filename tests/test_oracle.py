@@ -13,7 +13,7 @@ import torch
 
 import oracle
 from minillm_amd.validation import ModelShape, TAIL_SHAPES, make_activations, make_weights
-from _helpers import bits16, codes
+from _helpers import bits16, codes, crafted_sumsq_rows, sumsq_eps_sweep
 
 
 # ---------------------------------------------------------------------------- formats
@@ -246,6 +246,25 @@ def test_rmsnorm_closed_forms():
         normed = torch.tensor(np.float32(12.0) * inv).to(torch.bfloat16).float()
         assert y[0, 5] == _bf16_bits((w[5].float() * normed).to(torch.bfloat16).reshape(1))[0]
         assert (y[0, np.arange(width) != 5] & 0x7FFF).max() == 0   # zeros stay zero
+
+
+def test_rmsnorm_summation_order_closed_forms():
+    """The oracle's sum of squares on rows that make each part of the reference's order
+    visible (see _helpers.crafted_sumsq_rows), at block widths 512, 256, 32 (rows 1, 2, 16 of 2560),
+    256 (3 rows of 1024) and 32 (one row of 128)."""
+
+    for rows, width in [(1, 2560), (2, 2560), (16, 2560), (3, 1024), (1, 128)]:
+        bw = oracle.rmsnorm_block_width(rows, width)
+        for name, x, expect in crafted_sumsq_rows(rows, width, bw):
+            got = oracle.rmsnorm_sumsq(_bf16_bits(x))
+            assert np.array_equal(got, np.full(rows, expect, np.float32)), (name, rows, width, got[0], expect)
+        # The eps sweep the GPU test runs over these rows separates each closed-form sum from
+        # the sums the plausible other orders give (see sumsq_eps_sweep).
+        for name, x, expect in crafted_sumsq_rows(rows, width, bw):
+            sumsq_eps_sweep(width, expect, name)
+        # Sums that are exact in any order: the order cannot matter.
+        x = torch.full((rows, width), 3.0, dtype=torch.bfloat16)
+        assert np.array_equal(oracle.rmsnorm_sumsq(_bf16_bits(x)), np.full(rows, 9.0 * width, np.float32))
 
 
 def test_rmsnorm_matches_torch_within_one_ulp_and_residual_sum_is_exact():
