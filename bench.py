@@ -281,10 +281,10 @@ def bench_decode_layers(torch, fp8, stream, args, weights, projs):
     """The decode linears as a model runs them, chained over the rotating weight sets (one
     set per layer): residual add + RMSNorm + quantizer -> qkv GEMM; the q columns (the
     attention stand-in) -> quantizer + o_proj GEMM; residual add + RMSNorm + quantizer ->
-    gate_up GEMM; SiLU*up + quantizer -> down GEMM.  Seven launches per layer up to 8 rows
-    (the o_proj linear then quantizes inside its GEMM), eight above; none of them a
-    standalone quantizer in front of qkv, gate_up or down.  Reported: time per layer and the
-    layer's weight bytes per second."""
+    gate_up GEMM; SiLU*up + quantizer -> down GEMM.  Five launches per layer up to 8 rows
+    (the two norms, their quantizers and the o_proj quantizer run inside the GEMM launches),
+    eight above; none of them a standalone quantizer in front of qkv, gate_up or down.
+    Reported: time per layer and the layer's weight bytes per second."""
 
     m, hidden, eps = args.decode_m, 2560, 1e-6
     gen = torch.Generator().manual_seed(SEED + 3)
@@ -308,7 +308,7 @@ def bench_decode_layers(torch, fp8, stream, args, weights, projs):
     ms = timed_graph(torch, stream, chain, len(weights), args.steps, args.warmup, args.eager)
     nbytes = sum(p.n * p.k + 4 * ((p.n + 127) // 128) * ((p.k + 127) // 128) for p in projs)
     return {"us_per_layer": round(ms * 1e3, 2), "weight_gbps": round(nbytes / (ms * 1e6), 1),
-            "launches_per_layer": 7 if m <= 8 else 8}
+            "launches_per_layer": 5 if m <= 8 else 8}
 
 
 def bench_rmsnorm_quant(torch, fp8, stream, args):

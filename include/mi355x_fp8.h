@@ -185,6 +185,24 @@ int mi355x_fp8_rmsnorm_quant(const void* x, int x_dtype, int64_t M, int64_t K, i
                              int64_t ldq, int64_t kpad, float* s, int64_t s_sm, int64_t s_sk,
                              void* stream);
 
+/* Residual add + RMSNorm + activation quantizer + block GEMM in one launch, at decode sizes:
+ * out = fp8_linear(rms_norm(x [+ residual])) for bf16 x and bf16 out.  It replaces the pair
+ * the reference runs for the q/k/v and gate/up projections, rms_norm
+ * (engine/kernels/fused.py:165-199) followed by sm89_fp8_linear (engine/kernels/
+ * sm89_fp8.py:444-528), and gives the bits of this library's two-launch form of that pair
+ * (mi355x_fp8_rmsnorm_quant, then mi355x_fp8_block_gemm on its q and scales); residual_out
+ * receives bf16(x + residual) as there.  Each workgroup of the weight-streaming kernel
+ * recomputes the rows' norms, so this pays only at few rows: it returns
+ * MI355X_FP8_ERR_UNSUPPORTED, having launched nothing, when the call does not fit one launch
+ * (more than 8 rows, K not a multiple of 256 or above 2560, rows not 16-byte aligned, or a
+ * shape the decode kernel does not take), and the caller then runs the two launches.
+ * Operands as in mi355x_fp8_rmsnorm_quant (x, residual, norm weight) and mi355x_fp8_linear
+ * (w, ws, out). */
+int mi355x_fp8_rmsnorm_linear(const void* x, int64_t M, int64_t K, int64_t sxm, const void* residual, int64_t ldr,
+                              void* residual_out, int64_t ldro, const void* norm_weight, float eps, const uint8_t* w,
+                              int64_t ldw, const float* ws, int64_t ws_sn, int64_t ws_sk, int64_t N, void* out,
+                              int64_t ldo, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -117,6 +117,24 @@ int mi355x_fp8_rmsnorm_quant(const void* x, int x_dtype, int64_t M, int64_t K, i
                               static_cast<hipStream_t>(stream));
 }
 
+int mi355x_fp8_rmsnorm_linear(const void* x, int64_t M, int64_t K, int64_t sxm, const void* residual, int64_t ldr,
+                              void* residual_out, int64_t ldro, const void* norm_weight, float eps, const uint8_t* w,
+                              int64_t ldw, const float* ws, int64_t ws_sn, int64_t ws_sk, int64_t N, void* out,
+                              int64_t ldo, void* stream) {
+  if (M < 0 || N < 0 || K < 128 || K % 4 != 0 || sxm < K || ldw < K || ldo < N ||
+      (residual != nullptr && (ldr < K || residual_out == nullptr || ldro < K)))
+    return MI355X_FP8_ERR_INVALID;
+  if (M == 0 || N == 0) return MI355X_FP8_ERR_UNSUPPORTED;  // nothing to fuse: the caller's two launches handle it
+  if (!x || !norm_weight || !w || !ws || !out) return MI355X_FP8_ERR_INVALID;
+  GemmPlan plan;
+  const int st = plan_gemm(M, N, K, MI355X_FP8_CONFIG_AUTO, &plan);
+  if (st != MI355X_FP8_OK) return st;
+  return launch_norm_linear(plan, static_cast<const uint16_t*>(x), sxm, static_cast<const uint16_t*>(residual), ldr,
+                            static_cast<uint16_t*>(residual_out), ldro, static_cast<const uint16_t*>(norm_weight), eps,
+                            w, ldw, ws, ws_sn, ws_sk, static_cast<uint16_t*>(out), ldo, M, N, K,
+                            static_cast<hipStream_t>(stream));
+}
+
 size_t mi355x_fp8_block_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int config) {
   GemmPlan plan;
   if (plan_gemm(M, N, K, config, &plan) != MI355X_FP8_OK) return 0;

@@ -185,12 +185,78 @@ __global__ __launch_bounds__(kStreamWaves * 64) void stream_rounds_kernel(
 // a workgroup owns exactly 16 AF rows with 8 % AF == 0, inside one block.
 extern __shared__ float4 stream_fold_lds[];
 
-template <int NT, int AF, bool ALIGNED, bool RAGGED, typename OutT, typename XIn = uint8_t, int QT = 16>
+// The RMSNorm in front of a one-launch decode linear (stream_gemm_kernel with NORM): x is
+// the norm's input, `res` the residual added to it first (or null), `sum` receives
+// bf16(x + res) (or null), `w` is the norm weight; bw is the reduction's block width
+// (rmsnorm_block_width).
+struct NormArgs {
+  const uint16_t* res = nullptr;
+  int64_t ldr = 0;
+  uint16_t* sum = nullptr;
+  int64_t lds = 0;
+  const uint16_t* w = nullptr;
+  float eps = 0.0f;
+  float inv_k = 0.0f;
+  int bw = 0;
+};
+constexpr size_t kNormLds = 160 * 1024;  // a CU's whole LDS (one workgroup per CU)
+constexpr int kNormMaxVec = 10;  // vectors of 4 elements per lane: K <= 2560 (the registers it holds)
+
+__device__ __forceinline__ float bf16_bits_val(uint32_t b) { return __uint_as_float((b & 0xffffu) << 16); }
+__device__ __forceinline__ uint32_t bf16_add_pair(uint32_t x, uint32_t r) {
+  return f32_to_bf16_bits(bf16_bits_val(x) + bf16_bits_val(r)) |
+         (static_cast<uint32_t>(f32_to_bf16_bits(bf16_bits_val(x >> 16) + bf16_bits_val(r >> 16))) << 16);
+}
+
+// One row's 1 / sqrt(mean(x^2) + eps) in the reference's order (engine/kernels/fused.py:
+// 95-116, the tree of fused.py:61-75), the same additions rmsnorm_quant_kernel makes: lane l
+// holds vectors v = l + 64 i (i < nv), which are virtual thread t = v mod bw's vectors in
+// order; thread t = l + 64 j keeps four accumulators, combined ((a0 + a1) + a2) + a3; the
+// partials fold as s[t] += s[t + h] for h = bw/2 .. 64 inside the lane, then .. 1 across lanes.
+// xv holds bf16(x + residual) on return.
+template <int J>
+__device__ __forceinline__ float norm_row_inv(const uint2 (&xv)[kNormMaxVec], int nv, int lane, const NormArgs& na) {
+  float a[J][4];
+#pragma unroll
+  for (int j = 0; j < J; ++j)
+#pragma unroll
+    for (int c = 0; c < 4; ++c) a[j][c] = 0.0f;
+#pragma unroll
+  for (int i = 0; i < kNormMaxVec; ++i) {
+    if (i < nv) {
+      const uint32_t w2[2] = {xv[i].x, xv[i].y};
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const float e = bf16_bits_val(w2[c >> 1] >> (16 * (c & 1)));
+        a[i % J][c] = a[i % J][c] + e * e;
+      }
+    }
+  }
+  float part[J];
+#pragma unroll
+  for (int j = 0; j < J; ++j) part[j] = ((a[j][0] + a[j][1]) + a[j][2]) + a[j][3];
+#pragma unroll
+  for (int hj = J / 2; hj >= 1; hj >>= 1)
+#pragma unroll
+    for (int j = 0; j < hj; ++j) part[j] = part[j] + part[j + hj];
+  float ss = part[0];
+#pragma unroll
+  for (int h = 32; h >= 1; h >>= 1) {
+    const float other = __shfl_down(ss, h, 64);
+    if (lane < h) ss = ss + other;
+  }
+  ss = __shfl(ss, 0, 64);
+  const float var = ss * na.inv_k;
+  return static_cast<float>(1.0 / sqrt(static_cast<double>(var + na.eps)));
+}
+
+template <int NT, int AF, bool ALIGNED, bool RAGGED, typename OutT, typename XIn = uint8_t, int QT = 16,
+          bool NORM = false>
 __global__ __launch_bounds__(kStreamWaves * 64) void stream_gemm_kernel(
     const uint8_t* __restrict__ q, int64_t ldq, const float* __restrict__ as, int64_t as_sm,
     int64_t as_sk, const uint8_t* __restrict__ w, int64_t ldw, const float* __restrict__ ws,
     int64_t ws_sn, int64_t ws_sk, uint16_t* __restrict__ out, int64_t ldo, int64_t M, int64_t N,
-    int64_t K, int64_t KB, int rows_arg) {
+    int64_t K, int64_t KB, int rows_arg, NormArgs na = NormArgs{}) {
   static_assert(RAGGED || 8 % AF == 0, "a workgroup's rows lie in one weight-scale block");
   // XIn = uint8_t: q holds the quantized activations (ldq bytes per row) and as their scales.
   // XIn = bf16_t / f16_t: q holds the unquantized activations (ldq elements per row, 16-byte
@@ -210,6 +276,14 @@ __global__ __launch_bounds__(kStreamWaves * 64) void stream_gemm_kernel(
   constexpr bool kDense = kQuant && QT < 16;
   constexpr int kLPT = 64 / QT;  // lanes per token (dense pass)
   constexpr int kE = 128 / kLPT; // elements per lane (dense pass)
+  // NORM: x is an RMSNorm's input (bf16).  Waves 0 .. rows-1 each hold one row,
+  // x = bf16(x + residual), form its 1 / sqrt(mean(x^2) + eps) (norm_row_inv), code
+  // y = bf16(w * bf16(x * inv)) group by group and leave the codes and scales in LDS, where
+  // the K loop reads its operands: rmsnorm_quant_kernel's arithmetic and the quantizer's, so
+  // y, the codes, the scales and the output bits are those of rmsnorm_quant followed by the
+  // GEMM.  Each workgroup repeats this for the (at most 8) rows: 8 K-element rows of work
+  // against its own 16 AF K-element weight rows.
+  static_assert(!NORM || (kDense && std::is_same<XIn, bf16_t>::value), "RMSNorm: bf16 rows, up to 8 tokens");
   constexpr int kRows = 16 * AF;
   constexpr int kTok = 16 * NT;
   constexpr int kSB = RAGGED ? 2 : 1;
@@ -218,6 +292,12 @@ __global__ __launch_bounds__(kStreamWaves * 64) void stream_gemm_kernel(
   // [KB][kSB][kTok] scale products (first and last weight-scale block of the rows).
   float* part = reinterpret_cast<float*>(stream_fold_lds);
   float* scl = part + KB * kTok * kRows;
+  // NORM: the rows' 1 / rms [16], the norm weight [K] (bf16), then the rows' bf16(x + residual)
+  // [M][K + 8] (rows four banks apart).
+  [[maybe_unused]] float* ninv = scl + KB * kSB * kTok;
+  [[maybe_unused]] uint16_t* wl = reinterpret_cast<uint16_t*>(ninv + 16);
+  [[maybe_unused]] const int64_t xpitch = K + 8;
+  [[maybe_unused]] uint16_t* xs = wl + K;
 
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
@@ -242,29 +322,34 @@ __global__ __launch_bounds__(kStreamWaves * 64) void stream_gemm_kernel(
     float asv[NT], wsv[kSB];
     // Unquantized activations: elements 16 g .. +15 and 64 + 16 g .. +15 of token r (QT = 16),
     // or the kE elements of this lane's share (dense pass), as raw 16-bit pairs.
-    uint32_t xr[kQuant ? (kDense ? kE / 2 : 16) : 1];
+    uint32_t xr[kQuant && !NORM ? (kDense ? kE / 2 : 16) : 1];  // NORM: the rows come from LDS
   };
   auto load = [&](Operands& o, int64_t kb) {
     const int64_t k_lo = kb * kGroup + 16 * g;
     // Unquantized activations first: loads complete in issue order, so the wait for them
     // (before the group's quantization) then leaves this group's weight loads in flight, and
     // the quantization overlaps them (qkv and gate_up linears 0.2-0.4 us faster at 1-8 rows).
-    if constexpr (kDense) {
+    if constexpr (NORM) {
+      // The rows and the norm weight are in LDS (the norm pass put them there).
+    } else if constexpr (kDense) {
       // Token lane / kLPT, elements kb * 128 + (lane % kLPT) kE .. + kE - 1 (K % 16 == 0 and
       // kE divides 16, so a share is either whole or past K).
       const int t = lane / kLPT;
       const int64_t k = kb * kGroup + (lane % kLPT) * kE;
       const XT* xp = reinterpret_cast<const XT*>(q) + (m_base + t) * ldq + k;
       const bool ok = t < m_rows && k < K;
+      auto fetch = [&](const uint16_t* p, bool live, uint32_t* dst) {
 #pragma unroll
-      for (int c = 0; c < kE / 8; ++c) {
-        const uint4 v = ok ? reinterpret_cast<const uint4*>(xp)[c] : make_uint4(0u, 0u, 0u, 0u);
-        o.xr[4 * c] = v.x; o.xr[4 * c + 1] = v.y; o.xr[4 * c + 2] = v.z; o.xr[4 * c + 3] = v.w;
-      }
-      if constexpr (kE == 4) {
-        const uint2 v = ok ? *reinterpret_cast<const uint2*>(xp) : make_uint2(0u, 0u);
-        o.xr[0] = v.x; o.xr[1] = v.y;
-      }
+        for (int c = 0; c < kE / 8; ++c) {
+          const uint4 v = live ? reinterpret_cast<const uint4*>(p)[c] : make_uint4(0u, 0u, 0u, 0u);
+          dst[4 * c] = v.x; dst[4 * c + 1] = v.y; dst[4 * c + 2] = v.z; dst[4 * c + 3] = v.w;
+        }
+        if constexpr (kE == 4) {
+          const uint2 v = live ? *reinterpret_cast<const uint2*>(p) : make_uint2(0u, 0u);
+          dst[0] = v.x; dst[1] = v.y;
+        }
+      };
+      fetch(reinterpret_cast<const uint16_t*>(xp), ok, o.xr);
     } else if constexpr (kQuant) {
       const int64_t m = m_base + r;
       const XT* xrow = reinterpret_cast<const XT*>(q) + m * ldq;
@@ -295,13 +380,43 @@ __global__ __launch_bounds__(kStreamWaves * 64) void stream_gemm_kernel(
   };
   // The 1x128 quantizer on the lane's 32 elements of its token's K group; the four lanes of a
   // token (g = 0..3) hold the whole group, so the amax takes two cross-lane steps.
-  auto quantize = [&](Operands& o) {
+  auto quantize = [&](Operands& o, int64_t kb) {
     constexpr int kN = kDense ? kE : 32;  // elements this lane quantizes
     float t[kN];
+    if constexpr (NORM) {
+      // y = bf16(w * bf16(x * inv)) from the rows the norm pass left in LDS
+      // (rmsnorm_quant_kernel's pass 2); the slice's padding tokens quantize zeros.
+      const int tok = lane / kLPT;
+      const int64_t k = kb * kGroup + (lane % kLPT) * kE;
+      const bool live = tok < m_rows;
+      const float inv = live ? ninv[tok] : 0.0f;
+      uint32_t xw[kE / 2], ww[kE / 2];
 #pragma unroll
-    for (int e = 0; e < kN / 2; ++e) {
-      t[2 * e] = to_f32(XT{static_cast<uint16_t>(o.xr[e] & 0xffffu)});
-      t[2 * e + 1] = to_f32(XT{static_cast<uint16_t>(o.xr[e] >> 16)});
+      for (int c = 0; c < kE / 2; c += (kE >= 8 ? 4 : 2)) {
+        if constexpr (kE >= 8) {
+          const uint4 xv = live ? *reinterpret_cast<const uint4*>(xs + tok * xpitch + k + 2 * c) : make_uint4(0u, 0u, 0u, 0u);
+          const uint4 wv = *reinterpret_cast<const uint4*>(wl + k + 2 * c);
+          xw[c] = xv.x; xw[c + 1] = xv.y; xw[c + 2] = xv.z; xw[c + 3] = xv.w;
+          ww[c] = wv.x; ww[c + 1] = wv.y; ww[c + 2] = wv.z; ww[c + 3] = wv.w;
+        } else {
+          const uint2 xv = live ? *reinterpret_cast<const uint2*>(xs + tok * xpitch + k + 2 * c) : make_uint2(0u, 0u);
+          const uint2 wv = *reinterpret_cast<const uint2*>(wl + k + 2 * c);
+          xw[c] = xv.x; xw[c + 1] = xv.y; ww[c] = wv.x; ww[c + 1] = wv.y;
+        }
+      }
+#pragma unroll
+      for (int e = 0; e < kN / 2; ++e)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const float normed = round_bf16(bf16_bits_val(xw[e] >> (16 * h)) * inv);
+          t[2 * e + h] = round_bf16(bf16_bits_val(ww[e] >> (16 * h)) * normed);
+        }
+    } else {
+#pragma unroll
+      for (int e = 0; e < kN / 2; ++e) {
+        t[2 * e] = to_f32(XT{static_cast<uint16_t>(o.xr[e] & 0xffffu)});
+        t[2 * e + 1] = to_f32(XT{static_cast<uint16_t>(o.xr[e] >> 16)});
+      }
     }
     float amax = 0.0f;
 #pragma unroll
@@ -345,7 +460,7 @@ __global__ __launch_bounds__(kStreamWaves * 64) void stream_gemm_kernel(
   // MFMA partials of group kb and their publication; `refill` loads group kb_next into the
   // registers just consumed (issued before the LDS writes, so it overlaps them).
   auto consume = [&](Operands& o, int64_t kb, int64_t kb_next) {
-    if constexpr (kQuant) quantize(o);
+    if constexpr (kQuant) quantize(o, kb);
     v4f p[AF][NT];
 #pragma unroll
     for (int i = 0; i < AF; ++i)
@@ -374,9 +489,62 @@ __global__ __launch_bounds__(kStreamWaves * 64) void stream_gemm_kernel(
   constexpr int kDepth = ALIGNED && NT == 1 && AF <= (kQuant ? 2 : 3) ? 2 : 1;
   constexpr int64_t kStep = static_cast<int64_t>(kStreamWaves) * kDepth;
   Operands ops[kDepth];
+  // NORM: each of the first rows waves loads its row (and residual) before the group loads
+  // below, so that its wait for them leaves the weight loads in flight (loads complete in
+  // issue order).
+  [[maybe_unused]] uint2 nxv[NORM ? kNormMaxVec : 1], nrv[NORM ? kNormMaxVec : 1];
+  [[maybe_unused]] uint4 nwv = make_uint4(0u, 0u, 0u, 0u);  // norm weight elements 8 tid .. +7
+  [[maybe_unused]] const int nv = NORM ? static_cast<int>(K / 256) : 0;
+  [[maybe_unused]] const bool nrow = NORM && wave_u < m_rows;
+  if constexpr (NORM) {
+    if (tid < K / 8) nwv = reinterpret_cast<const uint4*>(na.w)[tid];
+    if (nrow) {
+      const uint16_t* xrow = reinterpret_cast<const uint16_t*>(q) + (m_base + wave_u) * ldq;
+      const uint16_t* rrow = na.res != nullptr ? na.res + (m_base + wave_u) * na.ldr : nullptr;
+#pragma unroll
+      for (int i = 0; i < kNormMaxVec; ++i) {
+        if (i < nv) {
+          nxv[i] = *reinterpret_cast<const uint2*>(xrow + 4 * (lane + 64 * i));
+          if (rrow != nullptr) nrv[i] = *reinterpret_cast<const uint2*>(rrow + 4 * (lane + 64 * i));
+        }
+      }
+    }
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+  }
 #pragma unroll
   for (int d = 0; d < kDepth; ++d)
     if (wave_u + d * kStreamWaves < KB) load(ops[d], wave_u + d * kStreamWaves);
+  if constexpr (NORM) {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+    float inv = 0.0f;
+    if (nrow) {
+      const int64_t m = m_base + wave_u;
+      if (na.res != nullptr) {
+#pragma unroll
+        for (int i = 0; i < kNormMaxVec; ++i) {
+          if (i < nv) {
+            nxv[i] = make_uint2(bf16_add_pair(nxv[i].x, nrv[i].x), bf16_add_pair(nxv[i].y, nrv[i].y));
+            if (na.sum != nullptr && blockIdx.x == 0)
+              *reinterpret_cast<uint2*>(na.sum + m * na.lds + 4 * (lane + 64 * i)) = nxv[i];
+          }
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < kNormMaxVec; ++i)
+        if (i < nv) *reinterpret_cast<uint2*>(xs + wave_u * xpitch + 4 * (lane + 64 * i)) = nxv[i];
+      switch (na.bw) {
+        case 512: inv = norm_row_inv<8>(nxv, nv, lane, na); break;
+        case 256: inv = norm_row_inv<4>(nxv, nv, lane, na); break;
+        case 128: inv = norm_row_inv<2>(nxv, nv, lane, na); break;
+        default: inv = norm_row_inv<1>(nxv, nv, lane, na); break;
+      }
+    }
+    if (lane == 0 && nrow) ninv[wave_u] = inv;
+    if (tid < K / 8) reinterpret_cast<uint4*>(wl)[tid] = nwv;
+    __syncthreads();
+  }
   for (int64_t kb = wave_u; kb < KB; kb += kStep) {
 #pragma unroll
     for (int d = 0; d < kDepth; ++d) {
@@ -856,6 +1024,75 @@ static int launch_linear_stream_x(const GemmPlan& p, const XIn* x, int64_t sxm, 
     default: return launch_linear_stream_t<1, OutT, XIn>(MI355X_LIN_ARGS);
   }
 #undef MI355X_LIN_ARGS
+}
+
+// RMSNorm + linear in one launch (stream_gemm_kernel with NORM), bf16 in and out.
+template <int AF, int QT>
+static int launch_norm_linear_q(const GemmPlan& p, const bf16_t* x, int64_t sxm, const NormArgs& na,
+                                const uint8_t* w, int64_t ldw, const float* ws, int64_t ws_sn, int64_t ws_sk,
+                                uint16_t* out, int64_t ldo, int64_t M, int64_t N, int64_t K, hipStream_t stream) {
+  const int64_t kb = cdiv(K, kGroup);
+  const bool ragged = p.rows != 16 * AF || 8 % AF != 0;
+  // The fold buffer, the rows' 1 / rms, the norm weight and the M rows at pitch K + 8.
+  const size_t bytes = stream_fold_bytes(kb, AF, 1, ragged ? 2 : 1) + 16 * sizeof(float) +
+                       static_cast<size_t>(K + M * (K + 8)) * sizeof(uint16_t);
+  // The rows staged in LDS take the buffer past the two-per-CU budget: one workgroup per CU
+  // (a decode projection's stream grid holds about one per CU anyway) with all its LDS.
+  if (bytes > kNormLds) return MI355X_FP8_ERR_UNSUPPORTED;
+  const dim3 grid(static_cast<unsigned>(cdiv(N, p.rows)), 1, 1);
+  const uint8_t* xq = reinterpret_cast<const uint8_t*>(x);
+  if (ragged)
+    stream_gemm_kernel<1, AF, true, true, bf16_t, bf16_t, QT, true><<<grid, kStreamWaves * 64, bytes, stream>>>(
+        xq, sxm, nullptr, 0, 0, w, ldw, ws, ws_sn, ws_sk, out, ldo, M, N, K, kb, p.rows, na);
+  else if constexpr (8 % AF == 0)
+    stream_gemm_kernel<1, AF, true, false, bf16_t, bf16_t, QT, true><<<grid, kStreamWaves * 64, bytes, stream>>>(
+        xq, sxm, nullptr, 0, 0, w, ldw, ws, ws_sn, ws_sk, out, ldo, M, N, K, kb, p.rows, na);
+  return hipGetLastError() == hipSuccess ? MI355X_FP8_OK : MI355X_FP8_ERR_LAUNCH;
+}
+
+template <int QT>
+static int launch_norm_linear_af(const GemmPlan& p, const bf16_t* x, int64_t sxm, const NormArgs& na,
+                                 const uint8_t* w, int64_t ldw, const float* ws, int64_t ws_sn, int64_t ws_sk,
+                                 uint16_t* out, int64_t ldo, int64_t M, int64_t N, int64_t K, hipStream_t stream) {
+#define MI355X_NL_ARGS p, x, sxm, na, w, ldw, ws, ws_sn, ws_sk, out, ldo, M, N, K, stream
+  switch (p.row_tiles) {
+    case 5: return launch_norm_linear_q<5, QT>(MI355X_NL_ARGS);
+    case 4: return launch_norm_linear_q<4, QT>(MI355X_NL_ARGS);
+    case 3: return launch_norm_linear_q<3, QT>(MI355X_NL_ARGS);
+    case 2: return launch_norm_linear_q<2, QT>(MI355X_NL_ARGS);
+    default: return launch_norm_linear_q<1, QT>(MI355X_NL_ARGS);
+  }
+#undef MI355X_NL_ARGS
+}
+
+int launch_norm_linear(const GemmPlan& plan, const uint16_t* x, int64_t sxm, const uint16_t* res, int64_t ldr,
+                       uint16_t* res_out, int64_t ldro, const uint16_t* norm_w, float eps, const uint8_t* w,
+                       int64_t ldw, const float* ws, int64_t ws_sn, int64_t ws_sk, uint16_t* out, int64_t ldo,
+                       int64_t M, int64_t N, int64_t K, hipStream_t stream) {
+  // One launch up to 8 rows (one lane-dense quantization pass), a row of at most 10 vectors
+  // of 4 elements per lane (K % 256 == 0, K <= 2560), a reduction of at least 64 virtual
+  // threads, 16-byte aligned rows throughout.
+  const auto a16 = [](const void* ptr) { return reinterpret_cast<uintptr_t>(ptr) % 16 == 0; };
+  if (plan.kernel != MI355X_FP8_CONFIG_STREAM || plan.token_tiles != 1 || plan.rows < 1 || M < 1 || M > 8 ||
+      N <= 0 || K % 256 != 0 || K / 256 > kNormMaxVec || sxm % 8 != 0 || ldw % 16 != 0 || !a16(x) || !a16(w) ||
+      !a16(norm_w) || (res != nullptr && (ldr % 8 != 0 || !a16(res) || res_out == nullptr || ldro % 8 != 0 ||
+                                           !a16(res_out))))
+    return MI355X_FP8_ERR_UNSUPPORTED;
+  const int bw = rmsnorm_block_width(M, K);
+  if (bw < 64 || bw > 512 || bw % 64 != 0) return MI355X_FP8_ERR_UNSUPPORTED;
+  NormArgs na;
+  na.res = res;
+  na.ldr = ldr;
+  na.sum = res_out;
+  na.lds = ldro;
+  na.w = norm_w;
+  na.eps = eps;
+  na.inv_k = 1.0f / static_cast<float>(K);
+  na.bw = bw;
+  const bf16_t* xb = reinterpret_cast<const bf16_t*>(x);
+  if (M <= 2) return launch_norm_linear_af<2>(plan, xb, sxm, na, w, ldw, ws, ws_sn, ws_sk, out, ldo, M, N, K, stream);
+  if (M <= 4) return launch_norm_linear_af<4>(plan, xb, sxm, na, w, ldw, ws, ws_sn, ws_sk, out, ldo, M, N, K, stream);
+  return launch_norm_linear_af<8>(plan, xb, sxm, na, w, ldw, ws, ws_sn, ws_sk, out, ldo, M, N, K, stream);
 }
 
 int launch_linear_stream(const GemmPlan& plan, const void* x, int x_dtype, int64_t sxm, int64_t sxk,

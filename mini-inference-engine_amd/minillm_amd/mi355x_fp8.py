@@ -568,15 +568,46 @@ def rmsnorm_quant_mi355x_fp8(x: torch.Tensor, weight: torch.Tensor, eps: float,
 def rmsnorm_linear_mi355x_fp8(x: torch.Tensor, norm_weight: torch.Tensor, eps: float, weight: torch.Tensor,
                               weight_scale_inv: torch.Tensor, residual: torch.Tensor | None = None,
                               output_dtype: torch.dtype | None = None):
-    """``fp8_linear(rms_norm(x [+ residual]), weight)`` with the norm and the activation
-    quantizer fused into one kernel (the q/k/v or gate/up projection of a Qwen3 layer).
-    Returns the projection, plus the residual sum when ``residual`` is given."""
+    """``fp8_linear(rms_norm(x [+ residual]), weight)`` (the q/k/v or gate/up projection of a
+    Qwen3 layer).  Returns the projection, plus the residual sum when ``residual`` is given.
 
-    outs = rmsnorm_quant_mi355x_fp8(x, norm_weight, eps, residual)
-    q, s = outs[0], outs[1]
+    Up to 8 rows (bf16 in and out, K a multiple of 256 up to 2560) the norm, the activation
+    quantizer and the GEMM run as one launch (the decode kernel recomputing the rows' norms);
+    otherwise the norm and the quantizer run fused in one kernel and the GEMM in a second.
+    Both give the same bits."""
+
     k = int(x.shape[-1])
     n = int(weight.shape[0])
     out_dtype = output_dtype or torch.bfloat16
+    x2 = x.reshape(-1, k)
+    if (out_dtype == torch.bfloat16 and x.dtype == torch.bfloat16 and norm_weight.dtype == torch.bfloat16
+            and x2.shape[0] <= 8 and x2.stride(-1) == 1 and weight.dtype == torch.float8_e4m3fn
+            and weight.stride(-1) == 1 and weight_scale_inv.dtype == torch.float32 and x.is_cuda
+            and mi355x_available(x.device) and weight.device == x.device and weight_scale_inv.device == x.device
+            and tuple(weight_scale_inv.shape) == (-(-n // 128), -(-k // 128)) and tuple(norm_weight.shape) == (k,)
+            and (residual is None or (residual.shape == x.shape and residual.dtype == torch.bfloat16))):
+        m = int(x2.shape[0])
+        out = torch.empty((m, n), device=x.device, dtype=out_dtype)
+        r2 = summed = None
+        if residual is not None:
+            r2 = residual.reshape(-1, k)
+            if r2.stride(-1) != 1:
+                r2 = r2.contiguous()
+            summed = torch.empty((m, k), device=x.device, dtype=x.dtype)
+        w1 = norm_weight.contiguous()
+        lib = _lib.load()
+        code = lib.mi355x_fp8_rmsnorm_linear(
+            x2.data_ptr(), m, k, x2.stride(0), None if r2 is None else r2.data_ptr(), 0 if r2 is None else r2.stride(0),
+            None if summed is None else summed.data_ptr(), k, w1.data_ptr(), float(eps), weight.data_ptr(),
+            weight.stride(0), weight_scale_inv.data_ptr(), weight_scale_inv.stride(0), weight_scale_inv.stride(1),
+            n, out.data_ptr(), out.stride(0), _stream_ptr(x.device))
+        if code != _lib.ERR_UNSUPPORTED:
+            _lib.check(code)
+            out = out.reshape(*x.shape[:-1], n)
+            return (out, summed.reshape(x.shape)) if residual is not None else out
+
+    outs = rmsnorm_quant_mi355x_fp8(x, norm_weight, eps, residual)
+    q, s = outs[0], outs[1]
     out = torch.empty((q.numel() // k, n), device=x.device, dtype=out_dtype)
     launch_block_gemm(q.reshape(-1, k), weight, out, s, weight_scale_inv)
     out = out.reshape(*x.shape[:-1], n)

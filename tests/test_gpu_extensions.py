@@ -10,6 +10,7 @@ import torch
 
 import oracle
 from _helpers import assert_close_rows, bits16, codes, crafted_sumsq_rows, oracle_linear, sumsq_eps_sweep
+from minillm_amd import _lib
 from minillm_amd import merged_projections as mp
 from minillm_amd import mi355x_fp8 as fp8
 from minillm_amd.validation import (
@@ -211,6 +212,59 @@ def test_rmsnorm_linear_equals_unfused(gpu):
     assert bitwise_equal(summed, summed2)
     assert bitwise_equal(out, fp8.mi355x_fp8_linear(y, wg, wsg, [128, 128]))
     assert_close_rows(out, oracle_linear(y.cpu(), w, ws))
+
+
+@pytest.mark.parametrize("shape", [ModelShape("qkv", 6144, 2560), ModelShape("gate_up", 19456, 2560),
+                                   ModelShape("k256", 1024, 256), ModelShape("k1024", 2560, 1024)],
+                         ids=lambda s: s.name)
+@pytest.mark.parametrize("rows", [1, 2, 3, 4, 5, 7, 8, 9])
+@pytest.mark.parametrize("with_residual", [False, True])
+def test_rmsnorm_linear_one_launch_equals_two(gpu, shape, rows, with_residual):
+    """Up to 8 rows the norm, the quantizer and the GEMM run as one launch (the decode kernel
+    recomputing each row's norm in the reference's order); its output and residual sum equal,
+    bit for bit, rmsnorm_quant followed by the GEMM on its codes and scales.  Rows carry
+    zeros, a huge value and -0.0; 9 rows take the two launches."""
+
+    _note("rmsnorm linear", shape.name, rows, with_residual)
+    gen = torch.Generator().manual_seed(rows * 7 + shape.k)
+    x = (torch.randn(rows, shape.k, generator=gen) * 2).to(torch.bfloat16)
+    x[0, :3] = torch.tensor([0.0, -0.0, 3000.0]).to(torch.bfloat16)
+    if rows > 1:
+        x[1] = 0.0
+    r = torch.randn(rows, shape.k, generator=gen).to(torch.bfloat16) if with_residual else None
+    nw = (torch.rand(shape.k, generator=gen) + 0.5).to(torch.bfloat16)
+    w, ws = make_weights(shape, 11)
+    xg, nwg, wg, wsg = x.to(gpu), nw.to(gpu), w.to(gpu), ws.to(gpu)
+    rg = None if r is None else r.to(gpu)
+    got = fp8.rmsnorm_linear_mi355x_fp8(xg, nwg, 1e-6, wg, wsg, residual=rg)
+    outs = fp8.rmsnorm_quant_mi355x_fp8(xg, nwg, 1e-6, rg, scale_layout="row")
+    ref = torch.empty((rows, shape.n), dtype=torch.bfloat16, device=gpu)
+    fp8.launch_block_gemm(outs[0], wg, ref, outs[1], wsg)
+    if with_residual:
+        assert bitwise_equal(got[0], ref), bit_mismatch_details(got[0], ref)
+        assert bitwise_equal(got[1], outs[2])
+    else:
+        assert bitwise_equal(got, ref), bit_mismatch_details(got, ref)
+    if rows <= 8:
+        # The one-launch entry point itself (the wrapper above falls back to two launches
+        # where the entry point answers unsupported): it must take these shapes.
+        direct = torch.empty((rows, shape.n), dtype=torch.bfloat16, device=gpu)
+        summed = torch.empty((rows, shape.k), dtype=torch.bfloat16, device=gpu) if with_residual else None
+        code = _lib.load().mi355x_fp8_rmsnorm_linear(
+            xg.data_ptr(), rows, shape.k, xg.stride(0), None if rg is None else rg.data_ptr(),
+            0 if rg is None else rg.stride(0), None if summed is None else summed.data_ptr(), shape.k,
+            nwg.data_ptr(), 1e-6, wg.data_ptr(), wg.stride(0), wsg.data_ptr(), wsg.stride(0), wsg.stride(1),
+            shape.n, direct.data_ptr(), direct.stride(0), torch.cuda.current_stream(gpu).cuda_stream)
+        assert code == 0, f"one-launch entry point returned {code}"
+        torch.cuda.synchronize(gpu)
+        assert bitwise_equal(direct, ref), bit_mismatch_details(direct, ref)
+        if with_residual:
+            assert bitwise_equal(summed, outs[2])
+    # A column view with a padded row stride: the same bits.
+    pad = torch.zeros(rows, shape.k + 64, dtype=torch.bfloat16, device=gpu)
+    pad[:, : shape.k] = xg
+    got2 = fp8.rmsnorm_linear_mi355x_fp8(pad[:, : shape.k], nwg, 1e-6, wg, wsg, residual=rg)
+    assert bitwise_equal(got2[0] if with_residual else got2, ref)
 
 
 def test_rmsnorm_quant_strided_rows(gpu):
