@@ -37,8 +37,8 @@ extern "C" {
                                        scales */
 /* One prefill kernel variant each (same preconditions as TILE256; otherwise the call returns
  * MI355X_FP8_ERR_UNSUPPORTED): the 128-row LDS-DMA kernel at width 64, 128 or 160, and the
- * 256-row kernel at width 128, 160, 192, 224 or 256.  Every config gives the same bits; these
- * exist for tuning and so that tests can reach each variant. */
+ * 256-row kernel and its 192-row form at width 128, 160, 192, 224 or 256.  Every config gives
+ * the same bits; these exist for tuning and so that tests can reach each variant. */
 #define MI355X_FP8_CONFIG_DMA128_64 4
 #define MI355X_FP8_CONFIG_DMA128_128 5
 #define MI355X_FP8_CONFIG_DMA128_160 6
@@ -47,6 +47,11 @@ extern "C" {
 #define MI355X_FP8_CONFIG_T256_192 9
 #define MI355X_FP8_CONFIG_T256_224 10
 #define MI355X_FP8_CONFIG_T256_256 11
+#define MI355X_FP8_CONFIG_T192_128 12
+#define MI355X_FP8_CONFIG_T192_160 13
+#define MI355X_FP8_CONFIG_T192_192 14
+#define MI355X_FP8_CONFIG_T192_224 15
+#define MI355X_FP8_CONFIG_T192_256 16
 
 /* Status codes. */
 #define MI355X_FP8_OK 0

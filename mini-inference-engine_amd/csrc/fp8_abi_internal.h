@@ -64,12 +64,13 @@ int launch_tile_dma(const uint8_t* q, int64_t ldq, const float* as, int64_t as_s
                     int64_t ldw, const float* ws, int64_t ws_sn, int64_t ws_sk, void* out, int out_dtype,
                     int64_t ldo, int64_t M, int64_t N, int64_t K, int bn, hipStream_t stream);
 
-// 256-row-tile prefill kernel (tile_gemm_256.hip); same preconditions as the DMA kernel.
-// bn: tile width, 256, 224 or 192 (two-stage LDS ring) or 160 or 128 (three-stage ring);
-// tile256_width picks the one with the lowest measured cost on `cus` CUs.
+// 256-row-tile prefill kernel (tile_gemm_256.hip), or its 192-row form (rows = 192); same
+// preconditions as the DMA kernel.  bn: tile width, 256, 224 or 192 (two-stage LDS ring) or
+// 160 or 128 (three-stage ring); tile256_width picks the 256-row width with the lowest
+// measured cost on `cus` CUs.
 int launch_tile256(const uint8_t* q, int64_t ldq, const float* as, int64_t as_sk, const uint8_t* w,
                    int64_t ldw, const float* ws, int64_t ws_sn, int64_t ws_sk, void* out, int out_dtype,
-                   int64_t ldo, int64_t M, int64_t N, int64_t K, int bn, hipStream_t stream);
+                   int64_t ldo, int64_t M, int64_t N, int64_t K, int bn, int rows, hipStream_t stream);
 int tile256_width(int64_t M, int64_t N, int64_t cus);
 // Whether the 256-row kernel's 32-bit byte offsets reach every byte of q and W.
 bool tile256_offsets_ok(int64_t ldq, int64_t ldw, int64_t M, int64_t N, int64_t K);

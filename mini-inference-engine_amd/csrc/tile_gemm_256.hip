@@ -90,33 +90,38 @@ __device__ __forceinline__ uint4* stage256() {
   }
 }
 
-// Tile geometry for width BN.
-template <int BN>
+// Tile geometry for width BN and J 16-row activation fragments per wave (tile rows 64 J:
+// 256 for J = 4, 192 for J = 3).
+template <int BN, int J>
 struct Geo {
   static_assert(BN % 32 == 0 && BN <= 256 && BN >= 128, "tile width");
+  static_assert(J == 3 || J == 4, "tile rows");
   static constexpr int kNI = BN / 32;             // 16-column MFMA tiles per wave
+  static constexpr int kJ = J;
+  static constexpr int kRows = 64 * J;            // tile rows
   static constexpr int kWBlocks = BN / 8;         // 1 KiB DMA blocks of the W tile
   static constexpr int kWPerWave = (kWBlocks + 7) / 8;
   static constexpr int kXOff = BN * 8;            // activation tile offset in the stage (uint4)
+  static constexpr int kNDma = kWPerWave + J;     // DMA instructions per wave per stage (X: 8 J blocks)
 };
 
 // Per-tile feed state of one lane.
 struct Src256 {
   uint32_t w[4];         // byte offset in W of this lane's 16-byte chunk of its rows of block 8 i + wave
-  uint32_t x[4];         // same in the activations (rows of block 8 i + wave)
+  uint32_t x[4];         // same in the activations (rows of block 8 i + wave, i < J)
   const float* as;       // activation scales (K-group-major), K group 0
   const float* ws_a;     // weight scales of the 128-column blocks the wave's columns touch, K group 0
   const float* ws_b;
-  int as_row[4];         // this lane's rows 64 wm + 16 j + r, clamped to M - 1
+  int as_row[4];         // this lane's rows 16 J wm + 16 j + r (j < J), clamped to M - 1
   uint32_t use_b;        // bit i: column tile i lies in block ws_b
   int vzero;             // 0 held in a VGPR, so that loads indexed by it are per-lane loads
 };
 
 // Fills stage S with K group kb.  W blocks past the tile (BN/8 not a multiple of 8) repeat
 // the last block: the two waves write identical bytes.
-template <int BN, int NS, int S>
+template <int BN, int J, int NS, int S>
 __device__ __forceinline__ void issue256(const Src256& src, const uint8_t* w, const uint8_t* q, int64_t kb, int wave) {
-  using G = Geo<BN>;
+  using G = Geo<BN, J>;
   uint4* st = stage256<NS, S>();
   const uint8_t* wk = w + kb * kGroup;
   const uint8_t* qk = q + kb * kGroup;
@@ -126,15 +131,15 @@ __device__ __forceinline__ void issue256(const Src256& src, const uint8_t* w, co
     dma16(wk, src.w[i], st + blk * 64);
   }
 #pragma unroll
-  for (int i = 0; i < 4; ++i) dma16(qk, src.x[i], st + G::kXOff + (i * 8 + wave) * 64);
+  for (int i = 0; i < J; ++i) dma16(qk, src.x[i], st + G::kXOff + (i * 8 + wave) * 64);
 }
 
 // One of the step's DMA instructions: t < kWPerWave loads W block 8 t + wave, the rest the
 // activation blocks.
-template <int BN, int NS, int S>
+template <int BN, int J, int NS, int S>
 __device__ __forceinline__ void issue_one(const Src256& src, const uint8_t* w, const uint8_t* q, int64_t kb, int wave,
                                           int t) {
-  using G = Geo<BN>;
+  using G = Geo<BN, J>;
   uint4* st = stage256<NS, S>();
   if (t < G::kWPerWave) {
     const int blk = (t * 8 + wave) < G::kWBlocks ? (t * 8 + wave) : (G::kWBlocks - 1);
@@ -151,7 +156,7 @@ __device__ __forceinline__ v8i frag(const uint4* tile, int row, int g) {
   return pack_v8i(p[g ^ (row & 7)], p[(g + 4) ^ (row & 7)]);
 }
 
-// Scales of one K group in registers: 4 activation scales (this lane's rows) and the two
+// Scales of one K group in registers: J activation scales (this lane's rows) and the two
 // weight scales the wave may need.
 struct Scales {
   float a[4];
@@ -171,41 +176,41 @@ struct Scales {
 // the MFMA it follows.  The eight scale products a_s[j] * w_s (two weight-scale blocks at
 // most) are formed once per step; each is the same single fp32 product as before, so the
 // folded values are unchanged bit for bit.
-template <int BN, int NS, int S, int NXT>
-__device__ __forceinline__ void compute256(v4f (&acc)[Geo<BN>::kNI][4], const Scales& sc_in, uint32_t use_b, int wm,
+template <int BN, int J, int NS, int S, int NXT>
+__device__ __forceinline__ void compute256(v4f (&acc)[BN / 32][J], const Scales& sc_in, uint32_t use_b, int wm,
                                            int wn, int r, int g, const Src256& src, const uint8_t* w,
                                            const uint8_t* q, int64_t kn, int wave) {
-  using G = Geo<BN>;
+  using G = Geo<BN, J>;
   constexpr int NI = G::kNI;
-  constexpr int NDMA = G::kWPerWave + 4;
+  constexpr int NDMA = G::kNDma;
   const uint4* st = stage256<NS, S>();
   const int wrow0 = wn * (BN / 2) + r;
-  float sa[4], sb[4];
+  float sa[J], sb[J];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
+  for (int j = 0; j < J; ++j) {
     sa[j] = sc_in.a[j] * sc_in.wa;
     sb[j] = sc_in.a[j] * sc_in.wb;
   }
   v8i a0 = frag<S>(st, wrow0, g);
-  v8i b[4];
+  v8i b[J];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) b[j] = frag<S>(st + G::kXOff, wm * 64 + 16 * j + r, g);
+  for (int j = 0; j < J; ++j) b[j] = frag<S>(st + G::kXOff, wm * 16 * J + 16 * j + r, g);
   v8i a1 = frag<S>(st, wrow0 + 16, g);
-  v4f p[2][4];
+  v4f p[2][J];
 #pragma unroll
   for (int i = 0; i <= NI; ++i) {
     v8i a2;
     if (i < NI) {
 #pragma unroll
       for (int t = 0; t < NDMA; ++t)
-        if ((t < NDMA / 2 ? 0 : NI / 2) == i) issue_one<BN, NS, NXT>(src, w, q, kn, wave, t);
+        if ((t < NDMA / 2 ? 0 : NI / 2) == i) issue_one<BN, J, NS, NXT>(src, w, q, kn, wave, t);
       if (i + 2 < NI) a2 = frag<S>(st, wrow0 + 16 * (i + 2), g);
     }
     // MFMA (i, j), then the fold of (i - 1, j), whose MFMA went out four MFMAs earlier; the
     // scheduling barriers keep that order, so no fold waits on the MFMA just issued.
     const bool ub = i > 0 && ((use_b >> (i - 1)) & 1);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < J; ++j) {
       if (i < NI) p[i & 1][j] = mfma_16x16x128_e4m3(a0, b[j]);
       if (i > 0) {
         const float sc = ub ? sb[j] : sa[j];
@@ -222,35 +227,35 @@ __device__ __forceinline__ void compute256(v4f (&acc)[Geo<BN>::kNI][4], const Sc
   }
 }
 
-// The unpipelined fold, for the 256-wide tiles: their accumulators leave no registers for a
-// second set of partials (the pipelined form spills there).
-template <int BN, int NS, int S, int NXT>
-__device__ __forceinline__ void compute256_plain(v4f (&acc)[Geo<BN>::kNI][4], const Scales& sc_in, uint32_t use_b, int wm,
-                                           int wn, int r, int g, const Src256& src, const uint8_t* w,
-                                           const uint8_t* q, int64_t kn, int wave) {
-  using G = Geo<BN>;
+// The unpipelined fold, for the 256-row, 256-wide tiles: their accumulators leave no registers
+// for a second set of partials (the pipelined form spills there; the 192-row form has room).
+template <int BN, int J, int NS, int S, int NXT>
+__device__ __forceinline__ void compute256_plain(v4f (&acc)[BN / 32][J], const Scales& sc_in, uint32_t use_b,
+                                                 int wm, int wn, int r, int g, const Src256& src, const uint8_t* w,
+                                                 const uint8_t* q, int64_t kn, int wave) {
+  using G = Geo<BN, J>;
   constexpr int NI = G::kNI;
-  constexpr int NDMA = G::kWPerWave + 4;
+  constexpr int NDMA = G::kNDma;
   const uint4* st = stage256<NS, S>();
   const int wrow0 = wn * (BN / 2) + r;
   v8i a0 = frag<S>(st, wrow0, g);
-  v8i b[4];
+  v8i b[J];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) b[j] = frag<S>(st + G::kXOff, wm * 64 + 16 * j + r, g);
+  for (int j = 0; j < J; ++j) b[j] = frag<S>(st + G::kXOff, wm * 16 * J + 16 * j + r, g);
   v8i a1 = frag<S>(st, wrow0 + 16, g);
 #pragma unroll
   for (int i = 0; i < NI; ++i) {
 #pragma unroll
     for (int t = 0; t < NDMA; ++t)
-      if ((t < NDMA / 2 ? 0 : NI / 2) == i) issue_one<BN, NS, NXT>(src, w, q, kn, wave, t);
+      if ((t < NDMA / 2 ? 0 : NI / 2) == i) issue_one<BN, J, NS, NXT>(src, w, q, kn, wave, t);
     v8i a2;
     if (i + 2 < NI) a2 = frag<S>(st, wrow0 + 16 * (i + 2), g);
     const float wsv = (use_b >> i) & 1 ? sc_in.wb : sc_in.wa;
-    v4f p[4];
+    v4f p[J];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) p[j] = mfma_16x16x128_e4m3(a0, b[j]);
+    for (int j = 0; j < J; ++j) p[j] = mfma_16x16x128_e4m3(a0, b[j]);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < J; ++j) {
       const float sc = sc_in.a[j] * wsv;
 #pragma unroll
       for (int v = 0; v < 4; ++v) acc[i][j][v] = __builtin_fmaf(p[j][v], sc, acc[i][j][v]);
@@ -271,9 +276,10 @@ __device__ __forceinline__ void sync_stage() {
   __builtin_amdgcn_s_barrier();
 }
 
+template <int J>
 __device__ __forceinline__ void load_scales(Scales& s, const Src256& src, int64_t kb, int64_t as_sk, int64_t ws_sk) {
 #pragma unroll
-  for (int j = 0; j < 4; ++j) s.a[j] = src.as[kb * as_sk + src.as_row[j]];
+  for (int j = 0; j < J; ++j) s.a[j] = src.as[kb * as_sk + src.as_row[j]];
   // Per-lane loads (vzero keeps them off the scalar unit: scalar loads share the LDS
   // counter, and waiting for one would wait for every fragment read).
   s.wa = src.ws_a[kb * ws_sk + src.vzero];
@@ -286,22 +292,22 @@ __device__ __forceinline__ void load_scales(Scales& s, const Src256& src, int64_
 // ahead (the one read in the previous step); the end-of-step wait leaves only that newest
 // batch in flight (loads complete in issue order).  Past the end of the range the loads
 // repeat its last group (the stage they fill is not read again).
-template <int BN, int NS, int CUR>
-__device__ __forceinline__ void step256(v4f (&acc)[Geo<BN>::kNI][4], const Scales& cur, Scales& next,
+template <int BN, int J, int NS, int CUR>
+__device__ __forceinline__ void step256(v4f (&acc)[BN / 32][J], const Scales& cur, Scales& next,
                                         const Src256& src, const uint8_t* w, const uint8_t* q, int64_t kb,
                                         int64_t khi, int64_t as_sk, int64_t ws_sk, int wave, int wm, int wn, int r,
                                         int g) {
-  constexpr int NDMA = Geo<BN>::kWPerWave + 4;
+  constexpr int NDMA = Geo<BN, J>::kNDma;
   const int64_t kn = kb + 1 < khi ? kb + 1 : khi - 1;
   const int64_t kd = kb + NS - 1 < khi ? kb + NS - 1 : khi - 1;
-  load_scales(next, src, kn, as_sk, ws_sk);
+  load_scales<J>(next, src, kn, as_sk, ws_sk);
   // Keep the scale loads ahead of the DMA loads (compiler and scheduler barriers).
   asm volatile("" ::: "memory");
   __builtin_amdgcn_sched_barrier(0);
-  if constexpr (BN == 256)
-    compute256_plain<BN, NS, CUR, (CUR + NS - 1) % NS>(acc, cur, src.use_b, wm, wn, r, g, src, w, q, kd, wave);
+  if constexpr (BN == 256 && J == 4)
+    compute256_plain<BN, J, NS, CUR, (CUR + NS - 1) % NS>(acc, cur, src.use_b, wm, wn, r, g, src, w, q, kd, wave);
   else
-    compute256<BN, NS, CUR, (CUR + NS - 1) % NS>(acc, cur, src.use_b, wm, wn, r, g, src, w, q, kd, wave);
+    compute256<BN, J, NS, CUR, (CUR + NS - 1) % NS>(acc, cur, src.use_b, wm, wn, r, g, src, w, q, kd, wave);
   // Every MFMA of the step is issued before the wait: the matrix core then works through
   // them while the wave waits for its DMA and the other waves (without this barrier the
   // scheduler moves the last MFMA groups behind s_barrier; measured 7 % slower on qkv).
@@ -336,10 +342,10 @@ struct Dims256 {
   int vec_out;  // out_vec_mode(out, ldo)
 };
 
-template <int BN>
+template <int BN, int J>
 __device__ __forceinline__ void setup_tile(Src256& src, const Dims256& d, int64_t m0, int64_t n0, int wave,
                                            int lane, int wm, int wn, int r) {
-  using G = Geo<BN>;
+  using G = Geo<BN, J>;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     if (i < G::kWPerWave) {
@@ -359,8 +365,8 @@ __device__ __forceinline__ void setup_tile(Src256& src, const Dims256& d, int64_
   src.as = d.as;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    const int64_t row = m0 + wm * 64 + 16 * j + r;
-    src.as_row[j] = static_cast<int>(row < d.M ? row : d.M - 1);
+    const int64_t row = m0 + wm * 16 * J + 16 * j + r;
+    src.as_row[j] = static_cast<int>(row < d.M ? row : d.M - 1);  // j >= J: unused
   }
   // The wave's columns [nw, nw + BN/2) touch at most two 128-column weight-scale blocks.
   const int64_t nw = n0 + wn * (BN / 2);
@@ -378,23 +384,23 @@ __device__ __forceinline__ void setup_tile(Src256& src, const Dims256& d, int64_
 
 // acc = the tile's products over K groups [klo, khi), in increasing order, through a ring
 // of NS (2 or 3) LDS stages.
-template <int BN, int NS>
-__device__ __forceinline__ void run_k(v4f (&acc)[Geo<BN>::kNI][4], const Src256& src, const Dims256& d, int64_t klo,
+template <int BN, int J, int NS>
+__device__ __forceinline__ void run_k(v4f (&acc)[BN / 32][J], const Src256& src, const Dims256& d, int64_t klo,
                                       int64_t khi, int wave, int wm, int wn, int r, int g) {
   static_assert(NS == 2 || (NS == 3 && BN <= kMaxBN3), "ring depth");
-  constexpr int NDMA = Geo<BN>::kWPerWave + 4;
+  constexpr int NDMA = Geo<BN, J>::kNDma;
 #pragma unroll
-  for (int i = 0; i < Geo<BN>::kNI; ++i)
+  for (int i = 0; i < Geo<BN, J>::kNI; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < J; ++j) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
 #define MI355X_STEP(CUR, SC, SN, KB) \
-  step256<BN, NS, CUR>(acc, SC, SN, src, d.w, d.q, KB, khi, d.as_sk, d.ws_sk, wave, wm, wn, r, g)
+  step256<BN, J, NS, CUR>(acc, SC, SN, src, d.w, d.q, KB, khi, d.as_sk, d.ws_sk, wave, wm, wn, r, g)
   if constexpr (NS == 2) {
     Scales s_even, s_odd;
-    load_scales(s_even, src, klo, d.as_sk, d.ws_sk);
+    load_scales<J>(s_even, src, klo, d.as_sk, d.ws_sk);
     asm volatile("" ::: "memory");
     __builtin_amdgcn_sched_barrier(0);
-    issue256<BN, 2, 0>(src, d.w, d.q, klo, wave);
+    issue256<BN, J, 2, 0>(src, d.w, d.q, klo, wave);
     __builtin_amdgcn_sched_barrier(0);
     sync_stage();
     int64_t kb = klo;
@@ -405,11 +411,11 @@ __device__ __forceinline__ void run_k(v4f (&acc)[Geo<BN>::kNI][4], const Src256&
     if (kb < khi) MI355X_STEP(0, s_even, s_odd, kb);
   } else {
     Scales s0, s1, s2;
-    load_scales(s0, src, klo, d.as_sk, d.ws_sk);
+    load_scales<J>(s0, src, klo, d.as_sk, d.ws_sk);
     asm volatile("" ::: "memory");
     __builtin_amdgcn_sched_barrier(0);
-    issue256<BN, 3, 0>(src, d.w, d.q, klo, wave);
-    issue256<BN, 3, 1>(src, d.w, d.q, klo + 1 < khi ? klo + 1 : khi - 1, wave);
+    issue256<BN, J, 3, 0>(src, d.w, d.q, klo, wave);
+    issue256<BN, J, 3, 1>(src, d.w, d.q, klo + 1 < khi ? klo + 1 : khi - 1, wave);
     __builtin_amdgcn_sched_barrier(0);
     sync_stage<NDMA>();  // stage 0 and the scales landed; stage 1 may still be in flight
     int64_t kb = klo;
@@ -424,17 +430,17 @@ __device__ __forceinline__ void run_k(v4f (&acc)[Geo<BN>::kNI][4], const Src256&
 #undef MI355X_STEP
 }
 
-// Lane holds out[m = m0 + 64 wm + 16 j + r][n = n0 + BN/2 wn + 16 i + 4 g + v].
-template <int BN, typename OutT>
-__device__ __forceinline__ void store_tile(const v4f (&acc)[Geo<BN>::kNI][4], const Dims256& d, int64_t m0,
+// Lane holds out[m = m0 + 16 J wm + 16 j + r][n = n0 + BN/2 wn + 16 i + 4 g + v].
+template <int BN, int J, typename OutT>
+__device__ __forceinline__ void store_tile(const v4f (&acc)[BN / 32][J], const Dims256& d, int64_t m0,
                                            int64_t n0, int wm, int wn, int r, int g) {
   const int64_t nw = n0 + wn * (BN / 2);
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int64_t m = m0 + wm * 64 + 16 * j + r;
+  for (int j = 0; j < J; ++j) {
+    const int64_t m = m0 + wm * 16 * J + 16 * j + r;
     if (m >= d.M) continue;
 #pragma unroll
-    for (int i = 0; i < Geo<BN>::kNI; ++i) {
+    for (int i = 0; i < Geo<BN, J>::kNI; ++i) {
       const int64_t n = nw + 16 * i + 4 * g;
       uint16_t h[4];
 #pragma unroll
@@ -452,34 +458,36 @@ __device__ __forceinline__ void store_tile(const v4f (&acc)[Geo<BN>::kNI][4], co
   }
 }
 
-// The epilogue through LDS (staged_index, fp8_common.h): rows 0-127 of the tile in ring stage
-// 0, rows 128-255 in stage 1.  Needs 16-byte aligned output rows (vec_out == 2).
-template <int BN, int NS, typename OutT>
-__device__ __forceinline__ void store_tile_lds(const v4f (&acc)[Geo<BN>::kNI][4], const Dims256& d, int64_t m0,
+// The epilogue through LDS (staged_index, fp8_common.h): the tile's first half of rows (32 J)
+// in ring stage 0, the second in stage 1.  Needs 16-byte aligned output rows (vec_out == 2).
+template <int BN, int J, int NS, typename OutT>
+__device__ __forceinline__ void store_tile_lds(const v4f (&acc)[BN / 32][J], const Dims256& d, int64_t m0,
                                                int64_t n0, int wm, int wn, int r, int g, int tid) {
+  constexpr int kHalf = 32 * J;
   uint16_t* r0 = reinterpret_cast<uint16_t*>(stage256<NS, 0>());
   uint16_t* r1 = reinterpret_cast<uint16_t*>(stage256<NS, 1>());
-  static_assert(128 * staged_pitch<BN>() * 2 <= (NS == 2 ? kStageU4 : kStage3U4) * 16, "staged rows fit a stage");
+  static_assert(kHalf * staged_pitch<BN>() * 2 <= (NS == 2 ? kStageU4 : kStage3U4) * 16, "staged rows fit a stage");
   __syncthreads();  // every wave is done with the ring
   uint16_t* reg = wm < 2 ? r0 : r1;
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
+  for (int j = 0; j < J; ++j) {
 #pragma unroll
-    for (int i = 0; i < Geo<BN>::kNI; ++i) {
+    for (int i = 0; i < Geo<BN, J>::kNI; ++i) {
       uint16_t h[4];
 #pragma unroll
       for (int v = 0; v < 4; ++v) h[v] = OutCvt<OutT>::cvt(acc[i][j][v]);
-      *reinterpret_cast<uint2*>(reg + staged_index<BN>((wm & 1) * 64 + 16 * j + r, wn * (BN / 2) + 16 * i + 4 * g)) =
+      *reinterpret_cast<uint2*>(reg + staged_index<BN>((wm & 1) * 16 * J + 16 * j + r, wn * (BN / 2) + 16 * i + 4 * g)) =
           make_uint2(h[0] | (static_cast<uint32_t>(h[1]) << 16), h[2] | (static_cast<uint32_t>(h[3]) << 16));
     }
   }
   __syncthreads();
   constexpr int C = BN / 8;  // 16-byte pieces per row
 #pragma unroll 4
-  for (int idx = tid; idx < kRowsT * C; idx += kT256Threads) {
+  for (int idx = tid; idx < 2 * kHalf * C; idx += kT256Threads) {
     const int row = idx / C, c = idx - (idx / C) * C;
     const int64_t m = m0 + row, n = n0 + 8 * c;
-    const uint4 val = *reinterpret_cast<const uint4*>((row < 128 ? r0 : r1) + staged_index<BN>(row & 127, 8 * c));
+    const uint4 val = *reinterpret_cast<const uint4*>(row < kHalf ? r0 + staged_index<BN>(row, 8 * c)
+                                                                   : r1 + staged_index<BN>(row - kHalf, 8 * c));
     if (m >= d.M) continue;
     uint16_t* dst = d.out + m * d.ldo + n;
     if (n + 8 <= d.N) {
@@ -492,7 +500,7 @@ __device__ __forceinline__ void store_tile_lds(const v4f (&acc)[Geo<BN>::kNI][4]
   }
 }
 
-template <int BN, int NS, typename OutT>
+template <int BN, int J, int NS, typename OutT>
 __global__ __launch_bounds__(kT256Threads, 2) void tile256_gemm_kernel(Dims256 d, int64_t tiles_m, int64_t tiles_n) {
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -505,24 +513,26 @@ __global__ __launch_bounds__(kT256Threads, 2) void tile256_gemm_kernel(Dims256 d
   tile_order(blockIdx.x, tiles_m, tiles_n, &tm, &tn);
   Src256 src;
   asm volatile("v_mov_b32 %0, 0" : "=v"(src.vzero));
-  setup_tile<BN>(src, d, tm * kRowsT, tn * BN, wave, lane, wm, wn, r);
-  v4f acc[Geo<BN>::kNI][4];
-  run_k<BN, NS>(acc, src, d, 0, d.KB, wave, wm, wn, r, g);
+  constexpr int RT = Geo<BN, J>::kRows;
+  setup_tile<BN, J>(src, d, tm * RT, tn * BN, wave, lane, wm, wn, r);
+  v4f acc[Geo<BN, J>::kNI][J];
+  run_k<BN, J, NS>(acc, src, d, 0, d.KB, wave, wm, wn, r, g);
   __builtin_amdgcn_s_waitcnt(0x70);  // no DMA may still target LDS when the workgroup ends
-  if (d.vec_out == 2) store_tile_lds<BN, NS, OutT>(acc, d, tm * kRowsT, tn * BN, wm, wn, r, g, tid);
-  else store_tile<BN, OutT>(acc, d, tm * kRowsT, tn * BN, wm, wn, r, g);
+  if (d.vec_out == 2) store_tile_lds<BN, J, NS, OutT>(acc, d, tm * RT, tn * BN, wm, wn, r, g, tid);
+  else store_tile<BN, J, OutT>(acc, d, tm * RT, tn * BN, wm, wn, r, g);
 }
 
-template <int BN, int NS>
+template <int BN, int J, int NS>
 int launch_bn(const Dims256& d, int out_dtype, hipStream_t stream) {
-  const int64_t tiles_m = (d.M + kRowsT - 1) / kRowsT;
+  constexpr int RT = Geo<BN, J>::kRows;
+  const int64_t tiles_m = (d.M + RT - 1) / RT;
   const int64_t tiles_n = (d.N + BN - 1) / BN;
   if (tiles_m * tiles_n > 0x7fffffffLL) return MI355X_FP8_ERR_UNSUPPORTED;
   const dim3 grid(static_cast<unsigned>(tiles_m * tiles_n));
   if (out_dtype == kBF16)
-    tile256_gemm_kernel<BN, NS, bf16_t><<<grid, kT256Threads, 0, stream>>>(d, tiles_m, tiles_n);
+    tile256_gemm_kernel<BN, J, NS, bf16_t><<<grid, kT256Threads, 0, stream>>>(d, tiles_m, tiles_n);
   else
-    tile256_gemm_kernel<BN, NS, f16_t><<<grid, kT256Threads, 0, stream>>>(d, tiles_m, tiles_n);
+    tile256_gemm_kernel<BN, J, NS, f16_t><<<grid, kT256Threads, 0, stream>>>(d, tiles_m, tiles_n);
   return hipGetLastError() == hipSuccess ? MI355X_FP8_OK : MI355X_FP8_ERR_LAUNCH;
 }
 
@@ -536,16 +546,27 @@ bool tile256_offsets_ok(int64_t ldq, int64_t ldw, int64_t M, int64_t N, int64_t 
 
 int launch_tile256(const uint8_t* q, int64_t ldq, const float* as, int64_t as_sk, const uint8_t* w,
                    int64_t ldw, const float* ws, int64_t ws_sn, int64_t ws_sk, void* out, int out_dtype,
-                   int64_t ldo, int64_t M, int64_t N, int64_t K, int bn, hipStream_t stream) {
+                   int64_t ldo, int64_t M, int64_t N, int64_t K, int bn, int rows, hipStream_t stream) {
   if (!tile256_offsets_ok(ldq, ldw, M, N, K)) return MI355X_FP8_ERR_UNSUPPORTED;
   const Dims256 d{q, as, w, ws, static_cast<uint16_t*>(out), ldq, as_sk, ldw, ws_sn, ws_sk, ldo, M, N, K / kGroup,
                   out_vec_mode(out, ldo)};
+  if (rows == 192) {
+    switch (bn) {
+      case 256: return launch_bn<256, 3, 2>(d, out_dtype, stream);
+      case 224: return launch_bn<224, 3, 2>(d, out_dtype, stream);
+      case 192: return launch_bn<192, 3, 2>(d, out_dtype, stream);
+      case 160: return launch_bn<160, 3, 3>(d, out_dtype, stream);
+      case 128: return launch_bn<128, 3, 3>(d, out_dtype, stream);
+      default: return MI355X_FP8_ERR_INVALID;
+    }
+  }
+  if (rows != 256) return MI355X_FP8_ERR_INVALID;
   switch (bn) {
-    case 256: return launch_bn<256, 2>(d, out_dtype, stream);
-    case 224: return launch_bn<224, 2>(d, out_dtype, stream);
-    case 192: return launch_bn<192, 2>(d, out_dtype, stream);
-    case 160: return launch_bn<160, 3>(d, out_dtype, stream);  // three-stage ring
-    case 128: return launch_bn<128, 3>(d, out_dtype, stream);
+    case 256: return launch_bn<256, 4, 2>(d, out_dtype, stream);
+    case 224: return launch_bn<224, 4, 2>(d, out_dtype, stream);
+    case 192: return launch_bn<192, 4, 2>(d, out_dtype, stream);
+    case 160: return launch_bn<160, 4, 3>(d, out_dtype, stream);  // three-stage ring
+    case 128: return launch_bn<128, 4, 3>(d, out_dtype, stream);
     default: return MI355X_FP8_ERR_INVALID;
   }
 }

@@ -72,6 +72,11 @@ GEMM_CONFIGS = (
     FP8GemmConfig("t256x192", _lib.CONFIG_T256_192, 256, 192),
     FP8GemmConfig("t256x224", _lib.CONFIG_T256_224, 256, 224),
     FP8GemmConfig("t256x256", _lib.CONFIG_T256_256, 256, 256),
+    FP8GemmConfig("t192x128", _lib.CONFIG_T192_128, 192, 128),
+    FP8GemmConfig("t192x160", _lib.CONFIG_T192_160, 192, 160),
+    FP8GemmConfig("t192x192", _lib.CONFIG_T192_192, 192, 192),
+    FP8GemmConfig("t192x224", _lib.CONFIG_T192_224, 192, 224),
+    FP8GemmConfig("t192x256", _lib.CONFIG_T192_256, 192, 256),
 )
 # Alias under the reference's name.
 SPLIT_GEMM_CONFIGS = GEMM_CONFIGS

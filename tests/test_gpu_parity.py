@@ -341,6 +341,9 @@ def test_prefill_2048_full_size(gpu, shape):
     (2048, 6144, 256),    # qkv width: 256x192 tiles
     (2048, 19456, 128),   # gate_up width: 256x224 tiles, last tile partial
     (2048, 8192, 128),    # 256x256 tiles
+    (536, 19456, 256),    # 192x256 tiles (3 x 192 rows against 3 x 256)
+    (320, 19456, 256),    # 192x160 tiles
+    (864, 6144, 256),     # 192x128 tiles
     # Ring depth: three stages when the tiles fit within the CUs, two otherwise; K of 1 to
     # 5 groups exercises the prologue and the unrolled loop's tail at both depths.
     (300, 200, 128),      # 3 stages, one K group
@@ -348,7 +351,7 @@ def test_prefill_2048_full_size(gpu, shape):
     (129, 640, 384),      # 3 stages, three K groups
     (200, 2560, 512),     # 3 stages, four K groups
     (536, 2560, 640),     # 3 stages, five K groups
-    (4096, 2560, 384),    # 2 stages (512 tiles), odd K-group count
+    (4096, 2560, 384),    # 256x160 tiles (256 tiles, one per CU; 128x160 costs the same), odd K-group count
 ], ids=lambda v: str(v))
 def test_prefill_tile_widths(gpu, rows, n, k):
     """Every tile width the prefill dispatch picks, against the oracle (the widths follow
@@ -367,6 +370,30 @@ def test_prefill_tile_widths(gpu, rows, n, k):
     reg = torch.empty_like(out)
     fp8.launch_block_gemm(q, wg, reg, s_row, wsg)
     assert bitwise_equal(reg, out), bit_mismatch_details(reg, out)
+
+
+@pytest.mark.parametrize("config", ["dma128x64", "dma128x128", "dma128x160"])
+def test_dma128_two_stage_ring(gpu, config):
+    """The 128-row DMA kernel's two-stage ring (two workgroups per CU), which it takes when its
+    tiles outnumber the CUs (4096 x 2560: 1280, 640 or 512 tiles), forced at every width: the
+    bits of the register-staged 128x128 kernel, and (every 97th row) within tolerance of the
+    oracle."""
+
+    rows, n, k = 4096, 2560, 384
+    cfg = {c.name: c for c in fp8.GEMM_CONFIGS}[config]
+    shape = ModelShape("w", n, k)
+    x = make_baseline_activations(rows, k, SEED + 5, outliers=True)
+    w, ws = make_baseline_weights(shape, SEED + 6)
+    wg, wsg = w.to(gpu), ws.to(gpu)
+    q, s_row = fp8.quantize_mi355x_fp8_activation(x.to(gpu))
+    _, s_km = fp8.quantize_mi355x_fp8_activation(x.to(gpu), scale_layout="kgroup")
+    out = torch.empty((rows, n), dtype=torch.bfloat16, device=gpu)
+    fp8.launch_block_gemm(q, wg, out, s_km, wsg, config=cfg)
+    reg = torch.empty_like(out)
+    fp8.launch_block_gemm(q, wg, reg, s_row, wsg)
+    assert bitwise_equal(reg, out), bit_mismatch_details(reg, out)
+    rows_checked = torch.arange(0, rows, 97)
+    assert_close_rows(out[rows_checked.to(gpu)], oracle_linear(x[rows_checked], w, ws))
 
 
 @pytest.mark.parametrize("shape", [ModelShape("kv", 1024, 2560), ModelShape("k264", 193, 264),
