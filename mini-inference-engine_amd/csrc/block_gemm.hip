@@ -214,8 +214,47 @@ __device__ __forceinline__ uint32_t bf16_add_pair(uint32_t x, uint32_t r) {
 // order; thread t = l + 64 j keeps four accumulators, combined ((a0 + a1) + a2) + a3; the
 // partials fold as s[t] += s[t + h] for h = bw/2 .. 64 inside the lane, then .. 1 across lanes.
 // xv holds bf16(x + residual) on return.
+// The halving tree s[t] += s[t + h], h = 32, 16, ..., 1, over the 64 lanes, with lane-to-lane
+// VALU moves instead of LDS shuffles: v_permlane32_swap and v_permlane16_swap bring lanes
+// t + 32 and t + 16 to lanes t, DPP row_shl:h brings t + h within each 16-lane row.  Lane t < h
+// adds lane t + h's value at every step, so lane 0 ends with the tree's sum, which goes to
+// every lane.
+__device__ __forceinline__ float tree_sum64(float s) {
+  s = s + __uint_as_float(__builtin_amdgcn_permlane32_swap(__float_as_uint(s), __float_as_uint(s), false, false)[1]);
+  s = s + __uint_as_float(__builtin_amdgcn_permlane16_swap(__float_as_uint(s), __float_as_uint(s), false, false)[1]);
+  s = s + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(s), 0x108, 0xf, 0xf, true));  // row_shl:8
+  s = s + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(s), 0x104, 0xf, 0xf, true));  // row_shl:4
+  s = s + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(s), 0x102, 0xf, 0xf, true));  // row_shl:2
+  s = s + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(s), 0x101, 0xf, 0xf, true));  // row_shl:1
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(s), 0));
+}
+
+// The maximum over each aligned group of L consecutive lanes (L a power of two), in every lane
+// of the group: quad permutes, then the half-row and row mirrors (each lane meets a lane of the
+// other half, already reduced), then the 16- and 32-lane swaps.  A maximum does not depend on
+// the pairing, so this equals any other reduction order.
+template <int L>
+__device__ __forceinline__ float group_max(float x) {
+  const auto dpp = [](float v, auto ctrl) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), decltype(ctrl)::value, 0xf, 0xf, false));
+  };
+  if constexpr (L >= 2) x = fmaxf(x, dpp(x, std::integral_constant<int, 0xB1>{}));   // quad_perm [1,0,3,2]
+  if constexpr (L >= 4) x = fmaxf(x, dpp(x, std::integral_constant<int, 0x4E>{}));   // quad_perm [2,3,0,1]
+  if constexpr (L >= 8) x = fmaxf(x, dpp(x, std::integral_constant<int, 0x141>{}));  // row_half_mirror
+  if constexpr (L >= 16) x = fmaxf(x, dpp(x, std::integral_constant<int, 0x140>{})); // row_mirror
+  if constexpr (L >= 32) {
+    const auto v = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    x = fmaxf(x, __uint_as_float(((threadIdx.x >> 4) & 1) ? v[0] : v[1]));
+  }
+  if constexpr (L >= 64) {
+    const auto v = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    x = fmaxf(x, __uint_as_float(((threadIdx.x >> 5) & 1) ? v[0] : v[1]));
+  }
+  return x;
+}
+
 template <int J>
-__device__ __forceinline__ float norm_row_inv(const uint2 (&xv)[kNormMaxVec], int nv, int lane, const NormArgs& na) {
+__device__ __forceinline__ float norm_row_inv(const uint2 (&xv)[kNormMaxVec], int nv, const NormArgs& na) {
   float a[J][4];
 #pragma unroll
   for (int j = 0; j < J; ++j)
@@ -239,13 +278,7 @@ __device__ __forceinline__ float norm_row_inv(const uint2 (&xv)[kNormMaxVec], in
   for (int hj = J / 2; hj >= 1; hj >>= 1)
 #pragma unroll
     for (int j = 0; j < hj; ++j) part[j] = part[j] + part[j + hj];
-  float ss = part[0];
-#pragma unroll
-  for (int h = 32; h >= 1; h >>= 1) {
-    const float other = __shfl_down(ss, h, 64);
-    if (lane < h) ss = ss + other;
-  }
-  ss = __shfl(ss, 0, 64);
+  const float ss = tree_sum64(part[0]);
   const float var = ss * na.inv_k;
   return static_cast<float>(1.0 / sqrt(static_cast<double>(var + na.eps)));
 }
@@ -422,8 +455,7 @@ __global__ __launch_bounds__(kStreamWaves * 64) void stream_gemm_kernel(
 #pragma unroll
     for (int e = 0; e < kN; ++e) amax = fmaxf(amax, fabsf(t[e]));
     if constexpr (kDense) {
-#pragma unroll
-      for (int off = 1; off < kLPT; off <<= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
+      amax = group_max<kLPT>(amax);
     } else {
       // The four lanes of a token (g = 0..3) hold the whole group.
       amax = fmaxf(amax, __shfl_xor(amax, 16));
@@ -535,10 +567,10 @@ __global__ __launch_bounds__(kStreamWaves * 64) void stream_gemm_kernel(
       for (int i = 0; i < kNormMaxVec; ++i)
         if (i < nv) *reinterpret_cast<uint2*>(xs + wave_u * xpitch + 4 * (lane + 64 * i)) = nxv[i];
       switch (na.bw) {
-        case 512: inv = norm_row_inv<8>(nxv, nv, lane, na); break;
-        case 256: inv = norm_row_inv<4>(nxv, nv, lane, na); break;
-        case 128: inv = norm_row_inv<2>(nxv, nv, lane, na); break;
-        default: inv = norm_row_inv<1>(nxv, nv, lane, na); break;
+        case 512: inv = norm_row_inv<8>(nxv, nv, na); break;
+        case 256: inv = norm_row_inv<4>(nxv, nv, na); break;
+        case 128: inv = norm_row_inv<2>(nxv, nv, na); break;
+        default: inv = norm_row_inv<1>(nxv, nv, na); break;
       }
     }
     if (lane == 0 && nrow) ninv[wave_u] = inv;
