@@ -197,6 +197,37 @@ def test_rmsnorm_summation_order_on_crafted_rows(gpu, rows, width):
             assert int(got[0, 0]) == int(bits16(y0.reshape(1))[0]), (name, eps)
 
 
+@pytest.mark.parametrize("rows,width", [(1, 2560), (2, 2560), (8, 2560), (3, 1024), (4, 1536), (1, 256)])
+def test_rmsnorm_linear_one_launch_summation_order(gpu, rows, width):
+    """The one-launch norm-linear's row sum (its own cross-lane tree) in the reference's
+    order: on the crafted rows whose sum of squares only that order gives, over the eps
+    sweep at which other sums change y (hence the group's scale, hence every output of the
+    row), its output equals the two launches' bit for bit (the two-launch norm is pinned to
+    the closed-form sums by test_rmsnorm_summation_order_on_crafted_rows)."""
+
+    _note("rmsnorm linear order", rows, width)
+    bw = oracle.rmsnorm_block_width(rows, width)
+    shape = ModelShape("c", 256, width)
+    w, ws = make_weights(shape, 17)
+    wg, wsg = w.to(gpu), ws.to(gpu)
+    nw = torch.ones(width, dtype=torch.bfloat16, device=gpu)
+    lib = _lib.load()
+    stream = torch.cuda.current_stream(gpu).cuda_stream
+    for name, x, expect in crafted_sumsq_rows(rows, width, bw):
+        xg = x.to(gpu)
+        for eps in sumsq_eps_sweep(width, expect, name):
+            direct = torch.empty((rows, shape.n), dtype=torch.bfloat16, device=gpu)
+            code = lib.mi355x_fp8_rmsnorm_linear(xg.data_ptr(), rows, width, xg.stride(0), None, 0, None, width,
+                                                 nw.data_ptr(), eps, wg.data_ptr(), wg.stride(0), wsg.data_ptr(),
+                                                 wsg.stride(0), wsg.stride(1), shape.n, direct.data_ptr(),
+                                                 direct.stride(0), stream)
+            assert code == 0, (name, eps, code)
+            q, sc = fp8.rmsnorm_quant_mi355x_fp8(xg, nw, eps, scale_layout="row")[:2]
+            ref = torch.empty_like(direct)
+            fp8.launch_block_gemm(q, wg, ref, sc, wsg)
+            assert bitwise_equal(direct, ref), (name, eps, bit_mismatch_details(direct, ref))
+
+
 def test_rmsnorm_linear_equals_unfused(gpu):
     """Norm + quantizer fused in front of the GEMM gives the same bits as the linear on the
     normalized activations (one quantizer, one GEMM arithmetic)."""
