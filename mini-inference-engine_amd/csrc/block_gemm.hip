@@ -214,45 +214,6 @@ __device__ __forceinline__ uint32_t bf16_add_pair(uint32_t x, uint32_t r) {
 // order; thread t = l + 64 j keeps four accumulators, combined ((a0 + a1) + a2) + a3; the
 // partials fold as s[t] += s[t + h] for h = bw/2 .. 64 inside the lane, then .. 1 across lanes.
 // xv holds bf16(x + residual) on return.
-// The halving tree s[t] += s[t + h], h = 32, 16, ..., 1, over the 64 lanes, with lane-to-lane
-// VALU moves instead of LDS shuffles: v_permlane32_swap and v_permlane16_swap bring lanes
-// t + 32 and t + 16 to lanes t, DPP row_shl:h brings t + h within each 16-lane row.  Lane t < h
-// adds lane t + h's value at every step, so lane 0 ends with the tree's sum, which goes to
-// every lane.
-__device__ __forceinline__ float tree_sum64(float s) {
-  s = s + __uint_as_float(__builtin_amdgcn_permlane32_swap(__float_as_uint(s), __float_as_uint(s), false, false)[1]);
-  s = s + __uint_as_float(__builtin_amdgcn_permlane16_swap(__float_as_uint(s), __float_as_uint(s), false, false)[1]);
-  s = s + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(s), 0x108, 0xf, 0xf, true));  // row_shl:8
-  s = s + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(s), 0x104, 0xf, 0xf, true));  // row_shl:4
-  s = s + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(s), 0x102, 0xf, 0xf, true));  // row_shl:2
-  s = s + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(s), 0x101, 0xf, 0xf, true));  // row_shl:1
-  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(s), 0));
-}
-
-// The maximum over each aligned group of L consecutive lanes (L a power of two), in every lane
-// of the group: quad permutes, then the half-row and row mirrors (each lane meets a lane of the
-// other half, already reduced), then the 16- and 32-lane swaps.  A maximum does not depend on
-// the pairing, so this equals any other reduction order.
-template <int L>
-__device__ __forceinline__ float group_max(float x) {
-  const auto dpp = [](float v, auto ctrl) {
-    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), decltype(ctrl)::value, 0xf, 0xf, false));
-  };
-  if constexpr (L >= 2) x = fmaxf(x, dpp(x, std::integral_constant<int, 0xB1>{}));   // quad_perm [1,0,3,2]
-  if constexpr (L >= 4) x = fmaxf(x, dpp(x, std::integral_constant<int, 0x4E>{}));   // quad_perm [2,3,0,1]
-  if constexpr (L >= 8) x = fmaxf(x, dpp(x, std::integral_constant<int, 0x141>{}));  // row_half_mirror
-  if constexpr (L >= 16) x = fmaxf(x, dpp(x, std::integral_constant<int, 0x140>{})); // row_mirror
-  if constexpr (L >= 32) {
-    const auto v = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-    x = fmaxf(x, __uint_as_float(((threadIdx.x >> 4) & 1) ? v[0] : v[1]));
-  }
-  if constexpr (L >= 64) {
-    const auto v = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-    x = fmaxf(x, __uint_as_float(((threadIdx.x >> 5) & 1) ? v[0] : v[1]));
-  }
-  return x;
-}
-
 template <int J>
 __device__ __forceinline__ float norm_row_inv(const uint2 (&xv)[kNormMaxVec], int nv, const NormArgs& na) {
   float a[J][4];
@@ -457,9 +418,8 @@ __global__ __launch_bounds__(kStreamWaves * 64) void stream_gemm_kernel(
     if constexpr (kDense) {
       amax = group_max<kLPT>(amax);
     } else {
-      // The four lanes of a token (g = 0..3) hold the whole group.
-      amax = fmaxf(amax, __shfl_xor(amax, 16));
-      amax = fmaxf(amax, __shfl_xor(amax, 32));
+      // The four lanes of a token (g = 0..3, lanes r + 16 g) hold the whole group.
+      amax = row_max(amax);
     }
     const float scale = amax / 448.0f;
     const float den = scale > 1e-12f ? scale : 1e-12f;

@@ -121,6 +121,57 @@ __device__ __forceinline__ void quant_codes(const float* t, float den, uint32_t*
   }
 }
 
+// Lane t's value from lane t ^ 16 (row_partner16) or t ^ 32 (row_partner32), through the
+// gfx950 lane swaps: with both operands the same register, the swap's second result holds the
+// odd rows' (upper half's) values in the even rows (lower half), its first result the reverse.
+__device__ __forceinline__ float row_partner16(float x) {
+  const auto v = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(((__lane_id() >> 4) & 1) ? v[0] : v[1]);
+}
+__device__ __forceinline__ float row_partner32(float x) {
+  const auto v = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(((__lane_id() >> 5) & 1) ? v[0] : v[1]);
+}
+
+// The halving tree s[t] += s[t + h], h = 32, 16, ..., 1, over the 64 lanes, with lane-to-lane
+// VALU moves instead of LDS shuffles: v_permlane32_swap and v_permlane16_swap bring lanes
+// t + 32 and t + 16 to lanes t, DPP row_shl:h brings t + h within each 16-lane row.  Lane t < h
+// adds lane t + h's value at every step, so lane 0 ends with the tree's sum, which goes to
+// every lane.
+__device__ __forceinline__ float tree_sum64(float s) {
+  s = s + __uint_as_float(__builtin_amdgcn_permlane32_swap(__float_as_uint(s), __float_as_uint(s), false, false)[1]);
+  s = s + __uint_as_float(__builtin_amdgcn_permlane16_swap(__float_as_uint(s), __float_as_uint(s), false, false)[1]);
+  s = s + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(s), 0x108, 0xf, 0xf, true));  // row_shl:8
+  s = s + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(s), 0x104, 0xf, 0xf, true));  // row_shl:4
+  s = s + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(s), 0x102, 0xf, 0xf, true));  // row_shl:2
+  s = s + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(s), 0x101, 0xf, 0xf, true));  // row_shl:1
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(s), 0));
+}
+
+// The maximum over each aligned group of L consecutive lanes (L a power of two), in every lane
+// of the group: quad permutes, then the half-row and row mirrors (each lane meets a lane of the
+// other half, already reduced), then the 16- and 32-lane swaps.  A maximum does not depend on
+// the pairing, so this equals any other reduction order.
+template <int L>
+__device__ __forceinline__ float group_max(float x) {
+  const auto dpp = [](float v, auto ctrl) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), decltype(ctrl)::value, 0xf, 0xf, false));
+  };
+  if constexpr (L >= 2) x = fmaxf(x, dpp(x, std::integral_constant<int, 0xB1>{}));   // quad_perm [1,0,3,2]
+  if constexpr (L >= 4) x = fmaxf(x, dpp(x, std::integral_constant<int, 0x4E>{}));   // quad_perm [2,3,0,1]
+  if constexpr (L >= 8) x = fmaxf(x, dpp(x, std::integral_constant<int, 0x141>{}));  // row_half_mirror
+  if constexpr (L >= 16) x = fmaxf(x, dpp(x, std::integral_constant<int, 0x140>{})); // row_mirror
+  if constexpr (L >= 32) x = fmaxf(x, row_partner16(x));
+  if constexpr (L >= 64) x = fmaxf(x, row_partner32(x));
+  return x;
+}
+
+// The maximum over the four lanes r, r + 16, r + 32, r + 48 (each 16-lane row's lane r).
+__device__ __forceinline__ float row_max(float x) {
+  x = fmaxf(x, row_partner16(x));
+  return fmaxf(x, row_partner32(x));
+}
+
 // The quantizer of one 128-wide group held by a 16-lane slice, 8 consecutive elements per
 // lane (reference engine/kernels/sm89_fp8.py:321-324): scale = amax / 448 (IEEE division,
 // stored raw), codes = e4m3fn(t / max(scale, 1e-12)), round-to-nearest-even, saturating.
@@ -130,8 +181,7 @@ __device__ __forceinline__ float quant_group16(const float (&t)[8], uint32_t (&p
   float amax = 0.0f;
 #pragma unroll
   for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(t[i]));
-#pragma unroll
-  for (int off = 8; off >= 1; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 16));
+  amax = group_max<16>(amax);
   const float scale = amax / 448.0f;
   const float den = scale > 1e-12f ? scale : 1e-12f;
   quant_codes<8>(t, den, packed);

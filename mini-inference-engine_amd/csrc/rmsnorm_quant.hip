@@ -175,12 +175,17 @@ __global__ __launch_bounds__(64 * kRnqWavesPerBlock) void rmsnorm_quant_kernel(
     ssum = v[0];
   }
   if (!live) return;  // no barrier follows
-  // Folds with h < 64: lane l adds lane l + h.
-  for (int h = (bw < 64 ? bw : 64) / 2; h >= 1; h >>= 1) {
-    const float other = __shfl_down(ssum, h, 64);
-    if (lane < h) ssum = __fadd_rn(ssum, other);
+  // Folds with h < 64: lane l adds lane l + h (tree_sum64: lane swaps and DPP; a reduction
+  // narrower than a wave keeps the shuffles).
+  if (bw >= 64) {
+    ssum = tree_sum64(ssum);
+  } else {
+    for (int h = bw / 2; h >= 1; h >>= 1) {
+      const float other = __shfl_down(ssum, h, 64);
+      if (lane < h) ssum = __fadd_rn(ssum, other);
+    }
+    ssum = __shfl(ssum, 0, 64);
   }
-  ssum = __shfl(ssum, 0, 64);
   const float var = __fmul_rn(ssum, inv_k);
   const float inv = static_cast<float>(1.0 / sqrt(static_cast<double>(__fadd_rn(var, eps))));
 
