@@ -36,8 +36,9 @@ extern "C" {
                                        == 0, 16-byte aligned q/w and K-group-major activation
                                        scales */
 /* One prefill kernel variant each (same preconditions as TILE256; otherwise the call returns
- * MI355X_FP8_ERR_UNSUPPORTED): the 128-row LDS-DMA kernel at width 64, 128 or 160, and the
- * 256-row kernel and its 192-row form at width 128, 160, 192, 224 or 256.  Every config gives
+ * MI355X_FP8_ERR_UNSUPPORTED): the 128-row LDS-DMA kernel at width 64, 128 or 160, the
+ * 256-row kernel and its 192-row form at width 128, 160, 192, 224 or 256, and the 64-row form
+ * of the LDS-DMA kernel at width 64 or 128.  Every config gives
  * the same bits; these exist for tuning and so that tests can reach each variant. */
 #define MI355X_FP8_CONFIG_DMA128_64 4
 #define MI355X_FP8_CONFIG_DMA128_128 5
@@ -52,6 +53,8 @@ extern "C" {
 #define MI355X_FP8_CONFIG_T192_192 14
 #define MI355X_FP8_CONFIG_T192_224 15
 #define MI355X_FP8_CONFIG_T192_256 16
+#define MI355X_FP8_CONFIG_DMA64_64 17
+#define MI355X_FP8_CONFIG_DMA64_128 18
 
 /* Status codes. */
 #define MI355X_FP8_OK 0

@@ -723,7 +723,7 @@ int plan_gemm(int64_t M, int64_t N, int64_t K, int config, GemmPlan* plan) {
                         (M <= 32 && cdiv(N, 16) <= 2 * device_cus());
     config = stream ? MI355X_FP8_CONFIG_STREAM : MI355X_FP8_CONFIG_TILE128;
   }
-  if (config < MI355X_FP8_CONFIG_STREAM || config > MI355X_FP8_CONFIG_T192_256) return MI355X_FP8_ERR_INVALID;
+  if (config < MI355X_FP8_CONFIG_STREAM || config > MI355X_FP8_CONFIG_DMA64_128) return MI355X_FP8_ERR_INVALID;
   plan->kernel = config;
   if (config != MI355X_FP8_CONFIG_STREAM) return MI355X_FP8_OK;
   // One 16-token tile per workgroup up to 16 rows, else slices of 32 rows (two tiles), one
@@ -791,10 +791,14 @@ int64_t device_cus() {
 //   128 x 160 / 128 / 64 (three stages)  21.4  17.5  12.5   (two per CU: 33.5  28.5  20.4)
 //   192 x 256 (two stages)               40.7
 //   192 x 160 / 128 (three stages)       26.0  24.5
+//   64 x 128 / 64 (three / four stages)  13.5   8.1   (two per CU: 22.0  13.5)
 // The 192-row tiles serve row counts just past a multiple of 256 or 128 (M = 536: 3 x 192
-// rows against 3 x 256).  Their figures are fitted to measured cases, set so that the model
-// keeps the older variant where the two measured within 3 % (gate_up at 176 rows, qkv at
-// 1024); listed last, they lose ties.
+// rows against 3 x 256), the 64-row ones small M whose 128-row tiles leave CUs idle (o_proj
+// and down up to 384 rows, qkv up to 128 and at 257-320).  Their figures are fitted to
+// measured cases with the weights streamed from HBM (40 rotating sets, beyond the MALL), set
+// so that the model keeps the older variant where the two measured within 4 %, or where the
+// 64-row tile re-reads the weights from HBM more than it gains (64 x 128 for o_proj and down
+// at 536 and 700 rows, gate_up at 160 and 176, qkv at 1024); listed last, they lose ties.
 // A last, partly filled wave costs 0.7 + 0.3 x its fill of a full one (a half-filled wave
 // measured 0.75-0.98).  Every kernel gives the same bits, so the choice may follow M.
 #ifndef MI355X_PREFILL_POLICY
@@ -810,6 +814,7 @@ constexpr TileVariant kTileVariants[] = {
     {256, 256, 46.5, 0.0}, {256, 224, 42.4, 0.0}, {256, 192, 37.4, 0.0}, {256, 160, 33.5, 0.0},
     {256, 128, 28.0, 0.0}, {128, 160, 21.4, 33.5}, {128, 128, 17.5, 28.5}, {128, 64, 12.5, 20.4},
     {192, 256, 40.7, 0.0}, {192, 160, 26.0, 0.0}, {192, 128, 24.5, 0.0},
+    {64, 128, 13.5, 22.0},  {64, 64, 8.1, 13.5},
 };
 
 double waves_cost(int64_t tiles, int64_t slots, double wave) {
@@ -824,7 +829,7 @@ double variant_cost(const TileVariant& v, int64_t M, int64_t N, int64_t cus) {
 }
 
 struct PrefillChoice {
-  int rows;  // 128: tile_gemm_dma; 192 or 256: tile_gemm_256
+  int rows;  // 64 or 128: tile_gemm_dma; 192 or 256: tile_gemm_256
   int bn;
 };
 
@@ -835,7 +840,7 @@ PrefillChoice choose_prefill(int64_t M, int64_t N, int64_t cus, bool rows256_ok)
   double best_cost = -1.0;
   for (const TileVariant& v : kTileVariants) {
     if ((MI355X_PREFILL_POLICY == 1 && v.rows != 256) || (MI355X_PREFILL_POLICY == 2 && v.rows != 128)) continue;
-    if (v.rows != 128 && !rows256_ok) continue;
+    if (v.rows > 128 && !rows256_ok) continue;
     const double cost = variant_cost(v, M, N, cus);
     if (best_cost < 0.0 || cost < best_cost) {
       best = {v.rows, v.bn};
@@ -950,11 +955,13 @@ int launch_block_gemm(const GemmPlan& plan, const uint8_t* q, int64_t ldq, const
   if (plan.kernel >= MI355X_FP8_CONFIG_DMA128_64) {
     // A forced variant: the LDS-DMA preconditions, and for 256- and 192-row tiles their 32-bit
     // offsets.
-    static constexpr int kWidth[] = {64, 128, 160, 128, 160, 192, 224, 256, 128, 160, 192, 224, 256};
+    static constexpr int kWidth[] = {64, 128, 160, 128, 160, 192, 224, 256, 128, 160, 192, 224, 256, 64, 128};
     const int bn = kWidth[plan.kernel - MI355X_FP8_CONFIG_DMA128_64];
     if (!dma_ok) return MI355X_FP8_ERR_UNSUPPORTED;
     if (plan.kernel <= MI355X_FP8_CONFIG_DMA128_160)
-      return launch_tile_dma(q, ldq, as, as_sk, w, ldw, ws, ws_sn, ws_sk, out, out_dtype, ldo, M, N, K, bn, stream);
+      return launch_tile_dma(q, ldq, as, as_sk, w, ldw, ws, ws_sn, ws_sk, out, out_dtype, ldo, M, N, K, bn, 128, stream);
+    if (plan.kernel >= MI355X_FP8_CONFIG_DMA64_64)
+      return launch_tile_dma(q, ldq, as, as_sk, w, ldw, ws, ws_sn, ws_sk, out, out_dtype, ldo, M, N, K, bn, 64, stream);
     const int rows = plan.kernel >= MI355X_FP8_CONFIG_T192_128 ? 192 : 256;
     return launch_tile256(q, ldq, as, as_sk, w, ldw, ws, ws_sn, ws_sk, out, out_dtype, ldo, M, N, K, bn, rows,
                           stream);
@@ -966,10 +973,11 @@ int launch_block_gemm(const GemmPlan& plan, const uint8_t* q, int64_t ldq, const
   }
   if (plan.kernel == MI355X_FP8_CONFIG_TILE128 && dma_ok) {
     const PrefillChoice c = choose_prefill(M, N, device_cus(), tile256_offsets_ok(ldq, ldw, M, N, K));
-    if (c.rows != 128)
+    if (c.rows > 128)
       return launch_tile256(q, ldq, as, as_sk, w, ldw, ws, ws_sn, ws_sk, out, out_dtype, ldo, M, N, K, c.bn, c.rows,
                             stream);
-    return launch_tile_dma(q, ldq, as, as_sk, w, ldw, ws, ws_sn, ws_sk, out, out_dtype, ldo, M, N, K, c.bn, stream);
+    return launch_tile_dma(q, ldq, as, as_sk, w, ldw, ws, ws_sn, ws_sk, out, out_dtype, ldo, M, N, K, c.bn, c.rows,
+                           stream);
   }
   const bool aligned = (K % 16) == 0 && (ldq % 16) == 0 && (ldw % 16) == 0 &&
                        (reinterpret_cast<uintptr_t>(q) % 16) == 0 &&

@@ -59,10 +59,10 @@ int launch_norm_linear(const GemmPlan& plan, const uint16_t* x, int64_t sxm, con
 // LDS-DMA pipelined prefill kernel (tile_gemm_dma.hip) and its preconditions.
 bool tile_dma_supported(const uint8_t* q, int64_t ldq, int64_t as_sm, int64_t as_sk, const uint8_t* w,
                         int64_t ldw, int64_t M, int64_t K);
-// bn: tile width, 64, 128 or 160.
+// bn: tile width, 64, 128 or 160; rows: tile rows, 128, or 64 (widths 64 and 128).
 int launch_tile_dma(const uint8_t* q, int64_t ldq, const float* as, int64_t as_sk, const uint8_t* w,
                     int64_t ldw, const float* ws, int64_t ws_sn, int64_t ws_sk, void* out, int out_dtype,
-                    int64_t ldo, int64_t M, int64_t N, int64_t K, int bn, hipStream_t stream);
+                    int64_t ldo, int64_t M, int64_t N, int64_t K, int bn, int rows, hipStream_t stream);
 
 // 256-row-tile prefill kernel (tile_gemm_256.hip), or its 192-row form (rows = 192); same
 // preconditions as the DMA kernel.  bn: tile width, 256, 224 or 192 (two-stage LDS ring) or

@@ -51,15 +51,18 @@ constexpr int kDmaThreads = 256;
 constexpr int kTileRows = 128;                          // activation rows per tile
 constexpr int kMaxBN = 160;                             // widest W tile (columns of the output tile)
 
-// Tile geometry for width BN (128 or 160): stage layout [W tile | X tile | scales].
-template <int BN>
+// Tile geometry for width BN (64, 128 or 160) and J 16-row activation fragments per wave
+// (tile rows 32 J: 128 for J = 4, 64 for J = 2): stage layout [W tile | X tile | scales].
+template <int BN, int J = 4>
 struct DmaGeo {
   static_assert(BN == 64 || BN == 128 || BN == 160, "tile width");
+  static_assert(J == 4 || J == 2, "tile rows");
   static constexpr int kNI = BN / 32;                  // 16-column MFMA tiles per wave (2 x 2 waves)
+  static constexpr int kRows = 32 * J;                 // activation rows of the tile
   static constexpr int kXOff = BN * 8;                 // uint4 offset of the activation tile
-  static constexpr int kScaleOff = (BN + kTileRows) * 8;
-  static constexpr int kDmaPerStage = BN / 32 + 4 + 1;  // DMA instructions per wave per stage
-  static constexpr int kStageU4 = (BN + kTileRows) * 8 + 64;  // one stage, in uint4
+  static constexpr int kScaleOff = (BN + kRows) * 8;
+  static constexpr int kDmaPerStage = BN / 32 + J + 1;  // DMA instructions per wave per stage
+  static constexpr int kStageU4 = (BN + kRows) * 8 + 64;  // one stage, in uint4
 };
 
 
@@ -117,7 +120,7 @@ struct DmaSources {
   const uint8_t* x;   // activation row m0 of the tile
   const float* as;    // activation scale of row m0, K group 0
   uint32_t woff[5];   // per-lane byte offsets from w of the W rows each DMA instruction fills
-  uint32_t xoff[4];   // the same for the activation rows, from x
+  uint32_t xoff[4];   // the same for the activation rows, from x (J of them)
   uint32_t soff;      // per-lane byte offset from as of the scale this lane stages
   const float* ws_a;  // weight scales of the (at most two) 128-column blocks the wave's columns touch
   const float* ws_b;
@@ -126,61 +129,61 @@ struct DmaSources {
 
 // The ring: STAGES stages of DmaGeo<BN>::kStageU4 each, in the kernel's own LDS array (sized
 // per instantiation, so the two-stage form still fits two workgroups per CU).
-template <int BN, int S>
+template <int BN, int S, int J = 4>
 __device__ __forceinline__ uint4* stage_ptr(uint4* ring) {
-  return ring + S * DmaGeo<BN>::kStageU4;
+  return ring + S * DmaGeo<BN, J>::kStageU4;
 }
 
 // DMA instruction d (0 .. kDmaPerStage-1) of a stage: W rows, then X rows, then scales.
-template <int BN, int S>
+template <int BN, int S, int J = 4>
 __device__ __forceinline__ void issue_one(uint4* ring, const DmaSources& src, int64_t kb, int64_t as_sk, int wave,
                                           int d) {
-  using G = DmaGeo<BN>;
-  uint4* st = stage_ptr<BN, S>(ring);
+  using G = DmaGeo<BN, J>;
+  uint4* st = stage_ptr<BN, S, J>(ring);
   const int64_t koff = kb * kGroup;
   if (d < G::kNI) dma16(src.w + koff, src.woff[d], st + (d * 4 + wave) * 64);
-  else if (d < G::kNI + 4) dma16(src.x + koff, src.xoff[d - G::kNI], st + G::kXOff + ((d - G::kNI) * 4 + wave) * 64);
+  else if (d < G::kNI + J) dma16(src.x + koff, src.xoff[d - G::kNI], st + G::kXOff + ((d - G::kNI) * 4 + wave) * 64);
   else dma4(src.as + kb * as_sk, src.soff, reinterpret_cast<float*>(st + G::kScaleOff) + wave * 64);
 }
 
-template <int BN, int S>
+template <int BN, int S, int J = 4>
 __device__ __forceinline__ void issue_stage(uint4* ring, const DmaSources& src, int64_t kb, int64_t as_sk, int wave) {
 #pragma unroll
-  for (int d = 0; d < DmaGeo<BN>::kDmaPerStage; ++d) issue_one<BN, S>(ring, src, kb, as_sk, wave, d);
+  for (int d = 0; d < DmaGeo<BN, J>::kDmaPerStage; ++d) issue_one<BN, S, J>(ring, src, kb, as_sk, wave, d);
 }
 
 // What the first MFMAs of a K step need, read from its stage one step early: the four
 // activation fragments, the first weight fragment, the activation scales and the weight
 // scales of the K group.
-template <int BN>
+template <int BN, int J = 4>
 struct StepHead {
-  v8i b[4];
+  v8i b[J];
   v8i a0;
-  float as_v[4];
+  float as_v[J];
   float wa, wb;
 };
 
-template <int BN, int S>
+template <int BN, int S, int J = 4>
 __device__ __forceinline__ v8i read_a(const uint4* ring, int i, int wn, int r, int g) {
-  const uint4* st = ring + S * DmaGeo<BN>::kStageU4;
+  const uint4* st = ring + S * DmaGeo<BN, J>::kStageU4;
   const int row = wn * (BN / 2) + 16 * i + r;
   return pack_v8i(st[row * 8 + (g ^ (row & 7))], st[row * 8 + ((g + 4) ^ (row & 7))]);
 }
 
-template <int BN, int S>
-__device__ __forceinline__ void read_head(const uint4* ring, StepHead<BN>& h, const DmaSources& src, int64_t kb,
+template <int BN, int S, int J = 4>
+__device__ __forceinline__ void read_head(const uint4* ring, StepHead<BN, J>& h, const DmaSources& src, int64_t kb,
                                           int64_t ws_sk, int wm, int wn, int r, int g) {
-  using G = DmaGeo<BN>;
+  using G = DmaGeo<BN, J>;
   const uint4* st = ring + S * G::kStageU4;
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int row = wm * 64 + 16 * j + r;
+  for (int j = 0; j < J; ++j) {
+    const int row = wm * 16 * J + 16 * j + r;
     h.b[j] = pack_v8i(st[G::kXOff + row * 8 + (g ^ (row & 7))], st[G::kXOff + row * 8 + ((g + 4) ^ (row & 7))]);
   }
-  h.a0 = read_a<BN, S>(ring, 0, wn, r, g);
+  h.a0 = read_a<BN, S, J>(ring, 0, wn, r, g);
   const float* sc_lds = reinterpret_cast<const float*>(st + G::kScaleOff);
 #pragma unroll
-  for (int j = 0; j < 4; ++j) h.as_v[j] = sc_lds[wm * 64 + 16 * j + r];
+  for (int j = 0; j < J; ++j) h.as_v[j] = sc_lds[wm * 16 * J + 16 * j + r];
   h.wa = src.ws_a[kb * ws_sk];
   h.wb = src.ws_b[kb * ws_sk];
 }
@@ -189,12 +192,12 @@ __device__ __forceinline__ void read_head(const uint4* ring, StepHead<BN>& h, co
 // the scale of the 128-column weight block the tile lies in.  Only BN = 160 lets a wave's
 // tiles straddle two blocks; the step forms both blocks' four products once (sa, sb), and each
 // tile picks its block's set on the scalar unit.
-template <int BN>
-__device__ __forceinline__ void fold_tile(v4f (&acc)[DmaGeo<BN>::kNI][4], const v4f (&p)[4], const float (&sa)[4],
-                                          const float (&sb)[4], uint32_t use_b, int i) {
+template <int BN, int J = 4>
+__device__ __forceinline__ void fold_tile(v4f (&acc)[BN / 32][J], const v4f (&p)[J], const float (&sa)[J],
+                                          const float (&sb)[J], uint32_t use_b, int i) {
   const bool ub = BN == 160 && ((use_b >> i) & 1);
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
+  for (int j = 0; j < J; ++j) {
     const float sc = ub ? sb[j] : sa[j];
 #pragma unroll
     for (int v = 0; v < 4; ++v) acc[i][j][v] = __builtin_fmaf(p[j][v], sc, acc[i][j][v]);
@@ -209,38 +212,38 @@ __device__ __forceinline__ void fold_tile(v4f (&acc)[DmaGeo<BN>::kNI][4], const 
 //   is refilled with K group kb+STAGES, and the last weight fragments are multiplied.
 // The LDS reads of each part so run behind MFMAs that do not depend on them.  Every
 // output element is still folded once per K group, in K order.
-template <int BN, int STAGES, int CUR>
-__device__ __forceinline__ void k_step(uint4* ring, v4f (&acc)[DmaGeo<BN>::kNI][4], StepHead<BN>& h, const DmaSources& src,
+template <int BN, int STAGES, int CUR, int J = 4>
+__device__ __forceinline__ void k_step(uint4* ring, v4f (&acc)[BN / 32][J], StepHead<BN, J>& h, const DmaSources& src,
                                        int64_t kb, int64_t KB, int64_t as_sk, int64_t ws_sk, int wave, int wm,
                                        int wn, int r, int g) {
-  using G = DmaGeo<BN>;
+  using G = DmaGeo<BN, J>;
   constexpr int NI = G::kNI;
   constexpr int NB = NI >= 4 ? 2 : 1;  // weight fragments multiplied after the barrier
   constexpr int NA = NI - NB;
   constexpr int NXT = (CUR + 1) % STAGES;
-  float sa[4], sb[4];
+  float sa[J], sb[J];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
+  for (int j = 0; j < J; ++j) {
     sa[j] = h.as_v[j] * h.wa;
     sb[j] = BN == 160 ? h.as_v[j] * h.wb : sa[j];
   }
   v8i a[NI];
   a[0] = h.a0;
-  v4f p[NI][4];
+  v4f p[NI][J];
 #pragma unroll
   for (int i = 0; i < NA; ++i) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) p[i][j] = mfma_16x16x128_e4m3(a[i], h.b[j]);
-    a[i + 1] = read_a<BN, CUR>(ring, i + 1, wn, r, g);
-    if (i > 0) fold_tile<BN>(acc, p[i - 1], sa, sb, src.use_b, i - 1);
+    for (int j = 0; j < J; ++j) p[i][j] = mfma_16x16x128_e4m3(a[i], h.b[j]);
+    a[i + 1] = read_a<BN, CUR, J>(ring, i + 1, wn, r, g);
+    if (i > 0) fold_tile<BN, J>(acc, p[i - 1], sa, sb, src.use_b, i - 1);
   }
 #pragma unroll
-  for (int i = NA + 1; i < NI; ++i) a[i] = read_a<BN, CUR>(ring, i, wn, r, g);
+  for (int i = NA + 1; i < NI; ++i) a[i] = read_a<BN, CUR, J>(ring, i, wn, r, g);
   // Per weight fragment of part A: its first MFMA, the two reads of the next fragment
   // (so that the wait before this MFMA covers only the fragment it needs), then the other
   // three MFMAs, each followed by folds of the fragment before.
 #pragma unroll
-  for (int i = 0; i < NA; ++i) {
+  for (int i = 0; i < (J == 4 ? NA : 0); ++i) {
     __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
     __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
     __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
@@ -254,32 +257,32 @@ __device__ __forceinline__ void k_step(uint4* ring, v4f (&acc)[DmaGeo<BN>::kNI][
   wait_vm_lgkm0<G::kDmaPerStage * (STAGES - 2)>();
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
-  StepHead<BN> nh;
-  read_head<BN, NXT>(ring, nh, src, kb + 1 < KB ? kb + 1 : KB - 1, ws_sk, wm, wn, r, g);
+  StepHead<BN, J> nh;
+  read_head<BN, NXT, J>(ring, nh, src, kb + 1 < KB ? kb + 1 : KB - 1, ws_sk, wm, wn, r, g);
   const int64_t ahead = kb + STAGES < KB ? kb + STAGES : KB - 1;
   // The refill's DMA instructions are spread over the MFMAs of part B.
-  constexpr int ND = G::kDmaPerStage, NM = 4 * NB;
+  constexpr int ND = G::kDmaPerStage, NM = J * NB;
 #pragma unroll
   for (int t = 0; t < NM; ++t) {
-    const int i = NA + t / 4, j = t % 4;
+    const int i = NA + t / J, j = t % J;
     p[i][j] = mfma_16x16x128_e4m3(a[i], h.b[j]);
 #pragma unroll
-    for (int d = t * ND / NM; d < (t + 1) * ND / NM; ++d) issue_one<BN, CUR>(ring, src, ahead, as_sk, wave, d);
-    if (j == 3 && i > 0) fold_tile<BN>(acc, p[i - 1], sa, sb, src.use_b, i - 1);
+    for (int d = t * ND / NM; d < (t + 1) * ND / NM; ++d) issue_one<BN, CUR, J>(ring, src, ahead, as_sk, wave, d);
+    if (j == J - 1 && i > 0) fold_tile<BN, J>(acc, p[i - 1], sa, sb, src.use_b, i - 1);
     __builtin_amdgcn_sched_barrier(0);
   }
-  fold_tile<BN>(acc, p[NI - 1], sa, sb, src.use_b, NI - 1);
+  fold_tile<BN, J>(acc, p[NI - 1], sa, sb, src.use_b, NI - 1);
   __builtin_amdgcn_sched_barrier(0);
   h = nh;
 }
 
-template <int STAGES, int BN, typename OutT>
+template <int STAGES, int BN, typename OutT, int J = 4>
 __global__ __launch_bounds__(kDmaThreads, STAGES == 2 ? 2 : 1) void tile_gemm_dma_kernel(
     const uint8_t* __restrict__ q, int64_t ldq, const float* __restrict__ as, int64_t as_sk,
     const uint8_t* __restrict__ w, int64_t ldw, const float* __restrict__ ws, int64_t ws_sn,
     int64_t ws_sk, uint16_t* __restrict__ out, int64_t ldo, int64_t M, int64_t N, int64_t KB,
     int64_t tiles_m, int64_t tiles_n, int vec_out) {
-  __shared__ uint4 ring[STAGES * DmaGeo<BN>::kStageU4];
+  __shared__ uint4 ring[STAGES * DmaGeo<BN, J>::kStageU4];
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63;
@@ -289,9 +292,9 @@ __global__ __launch_bounds__(kDmaThreads, STAGES == 2 ? 2 : 1) void tile_gemm_dm
   const int wn = wave >> 1;
   int64_t tm, tn;
   tile_of_dma(blockIdx.x, tiles_m, tiles_n, &tm, &tn);
-  using G = DmaGeo<BN>;
+  using G = DmaGeo<BN, J>;
   constexpr int NI = G::kNI;
-  const int64_t m0 = tm * kTileRows;
+  const int64_t m0 = tm * G::kRows;
   const int64_t n0 = tn * BN;
 
   DmaSources src;
@@ -304,14 +307,15 @@ __global__ __launch_bounds__(kDmaThreads, STAGES == 2 ? 2 : 1) void tile_gemm_dm
     const int c = (lane & 7) ^ (rr & 7);
     const int64_t wrow = (n0 + rr) < N ? rr : (N - 1 - n0);
     src.woff[i] = static_cast<uint32_t>(wrow * ldw + 16 * c);
-    if (i < 4) {
+    if (i < J) {
       const int64_t xrow = (m0 + rr) < M ? rr : (M - 1 - m0);
       src.xoff[i] = static_cast<uint32_t>(xrow * ldq + 16 * c);
     }
   }
   {
-    // Wave w stages the scales of tile rows 64 (w & 1) .. +63 (waves 2, 3 duplicate 0, 1).
-    const int64_t srow = (wave & 1) * 64 + lane;
+    // Wave w stages the scales of tile rows 64 (w & 1) .. +63 (waves 2, 3 duplicate 0, 1); a
+    // 64-row tile's are staged by every wave alike.
+    const int64_t srow = (J == 4 ? (wave & 1) * 64 : 0) + lane;
     src.soff = static_cast<uint32_t>(4 * (m0 + srow < M ? srow : M - 1 - m0));
   }
   {
@@ -329,26 +333,26 @@ __global__ __launch_bounds__(kDmaThreads, STAGES == 2 ? 2 : 1) void tile_gemm_dm
     src.use_b = use_b;
   }
 
-  v4f acc[NI][4];
+  v4f acc[NI][J];
 #pragma unroll
   for (int i = 0; i < NI; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < J; ++j) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
 
   static_assert(STAGES >= 2 && STAGES <= 6, "stages");
-  issue_stage<BN, 0>(ring, src, 0, as_sk, wave);
-  issue_stage<BN, 1>(ring, src, KB > 1 ? 1 : KB - 1, as_sk, wave);
-  if constexpr (STAGES >= 3) issue_stage<BN, 2>(ring, src, KB > 2 ? 2 : KB - 1, as_sk, wave);
-  if constexpr (STAGES >= 4) issue_stage<BN, 3>(ring, src, KB > 3 ? 3 : KB - 1, as_sk, wave);
-  if constexpr (STAGES >= 5) issue_stage<BN, 4>(ring, src, KB > 4 ? 4 : KB - 1, as_sk, wave);
-  if constexpr (STAGES >= 6) issue_stage<BN, 5>(ring, src, KB > 5 ? 5 : KB - 1, as_sk, wave);
+  issue_stage<BN, 0, J>(ring, src, 0, as_sk, wave);
+  issue_stage<BN, 1, J>(ring, src, KB > 1 ? 1 : KB - 1, as_sk, wave);
+  if constexpr (STAGES >= 3) issue_stage<BN, 2, J>(ring, src, KB > 2 ? 2 : KB - 1, as_sk, wave);
+  if constexpr (STAGES >= 4) issue_stage<BN, 3, J>(ring, src, KB > 3 ? 3 : KB - 1, as_sk, wave);
+  if constexpr (STAGES >= 5) issue_stage<BN, 4, J>(ring, src, KB > 4 ? 4 : KB - 1, as_sk, wave);
+  if constexpr (STAGES >= 6) issue_stage<BN, 5, J>(ring, src, KB > 5 ? 5 : KB - 1, as_sk, wave);
   wait_vm_lgkm0<G::kDmaPerStage * (STAGES - 1)>();
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
-  StepHead<BN> h;
-  read_head<BN, 0>(ring, h, src, 0, ws_sk, wm, wn, r, g);
+  StepHead<BN, J> h;
+  read_head<BN, 0, J>(ring, h, src, 0, ws_sk, wm, wn, r, g);
   int64_t kb = 0;
-#define MI355X_KSTEP(S, KBV) k_step<BN, STAGES, S>(ring, acc, h, src, KBV, KB, as_sk, ws_sk, wave, wm, wn, r, g)
+#define MI355X_KSTEP(S, KBV) k_step<BN, STAGES, S, J>(ring, acc, h, src, KBV, KB, as_sk, ws_sk, wave, wm, wn, r, g)
   for (; kb + STAGES <= KB; kb += STAGES) {
     MI355X_KSTEP(0, kb);
     MI355X_KSTEP(1, kb + 1);
@@ -371,14 +375,16 @@ __global__ __launch_bounds__(kDmaThreads, STAGES == 2 ? 2 : 1) void tile_gemm_dm
   wait_vm_lgkm0<0>();  // no DMA may still target LDS when the workgroup ends
 
   if (vec_out == 2) {
-    // Through LDS (staged_index, fp8_common.h): tile rows 0-63 in stage0, 64-127 in stage1.
-    static_assert(64 * staged_pitch<BN>() * 2 <= DmaGeo<BN>::kStageU4 * 16, "staged rows fit a stage");
+    // Through LDS (staged_index, fp8_common.h): the tile's first 16 J rows in stage0, the
+    // others in stage1.
+    constexpr int kHalf = 16 * J;
+    static_assert(kHalf * staged_pitch<BN>() * 2 <= G::kStageU4 * 16, "staged rows fit a stage");
     __syncthreads();  // every wave is done with the ring
-    uint4* const stage0 = stage_ptr<BN, 0>(ring);
-    uint4* const stage1 = stage_ptr<BN, 1>(ring);
+    uint4* const stage0 = stage_ptr<BN, 0, J>(ring);
+    uint4* const stage1 = stage_ptr<BN, 1, J>(ring);
     uint16_t* reg = reinterpret_cast<uint16_t*>(wm == 0 ? stage0 : stage1);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < J; ++j) {
 #pragma unroll
       for (int i = 0; i < NI; ++i) {
         uint16_t h[4];
@@ -390,14 +396,14 @@ __global__ __launch_bounds__(kDmaThreads, STAGES == 2 ? 2 : 1) void tile_gemm_dm
     }
     __syncthreads();
     constexpr int C = BN / 8;  // 16-byte pieces per row
-    static_assert((kTileRows * C) % kDmaThreads == 0, "whole passes");
+    static_assert((G::kRows * C) % kDmaThreads == 0, "whole passes");
 #pragma unroll
-    for (int it = 0; it < kTileRows * C / kDmaThreads; ++it) {
+    for (int it = 0; it < G::kRows * C / kDmaThreads; ++it) {
       const int idx = tid + it * kDmaThreads;
       const int row = idx / C, c = idx - (idx / C) * C;
       const int64_t m = m0 + row, n = n0 + 8 * c;
-      const uint16_t* reg_r = reinterpret_cast<const uint16_t*>(row < 64 ? stage0 : stage1);
-      const uint4 val = *reinterpret_cast<const uint4*>(reg_r + staged_index<BN>(row & 63, 8 * c));
+      const uint16_t* reg_r = reinterpret_cast<const uint16_t*>(row < kHalf ? stage0 : stage1);
+      const uint4 val = *reinterpret_cast<const uint4*>(reg_r + staged_index<BN>(row % kHalf, 8 * c));
       if (m >= M) continue;
       uint16_t* dst = out + m * ldo + n;
       if (n + 8 <= N) {
@@ -411,10 +417,10 @@ __global__ __launch_bounds__(kDmaThreads, STAGES == 2 ? 2 : 1) void tile_gemm_dm
     return;
   }
 
-  // Lane holds out[m = m0 + 64 wm + 16 j + r][n = n0 + BN/2 wn + 16 i + 4 g + v].
+  // Lane holds out[m = m0 + 16 J wm + 16 j + r][n = n0 + BN/2 wn + 16 i + 4 g + v].
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int64_t m = m0 + wm * 64 + 16 * j + r;
+  for (int j = 0; j < J; ++j) {
+    const int64_t m = m0 + wm * 16 * J + 16 * j + r;
     if (m >= M) continue;
 #pragma unroll
     for (int i = 0; i < NI; ++i) {
@@ -448,9 +454,10 @@ bool tile_dma_supported(const uint8_t* q, int64_t ldq, int64_t as_sm, int64_t as
 
 int launch_tile_dma(const uint8_t* q, int64_t ldq, const float* as, int64_t as_sk, const uint8_t* w,
                     int64_t ldw, const float* ws, int64_t ws_sn, int64_t ws_sk, void* out, int out_dtype,
-                    int64_t ldo, int64_t M, int64_t N, int64_t K, int bn, hipStream_t stream) {
+                    int64_t ldo, int64_t M, int64_t N, int64_t K, int bn, int rows, hipStream_t stream) {
   if (bn != 64 && bn != 128 && bn != 160) return MI355X_FP8_ERR_INVALID;
-  const int64_t tiles_m = (M + kTileRows - 1) / kTileRows;
+  if (rows != 128 && (rows != 64 || bn == 160)) return MI355X_FP8_ERR_INVALID;
+  const int64_t tiles_m = (M + rows - 1) / rows;
   const int64_t tiles_n = (N + bn - 1) / bn;
   if (tiles_m * tiles_n > 0x7fffffffLL) return MI355X_FP8_ERR_UNSUPPORTED;
   const int vec_out = out_vec_mode(out, ldo);
@@ -466,7 +473,21 @@ int launch_tile_dma(const uint8_t* q, int64_t ldq, const float* as, int64_t as_s
 #define MI355X_DMA_LAUNCH(ST, BN)                                                                                  \
   (out_dtype == kBF16 ? tile_gemm_dma_kernel<ST, BN, bf16_t><<<grid, kDmaThreads, 0, stream>>>(MI355X_DMA_ARGS) \
                       : tile_gemm_dma_kernel<ST, BN, f16_t><<<grid, kDmaThreads, 0, stream>>>(MI355X_DMA_ARGS))
-  if (!few) {
+#define MI355X_DMA_LAUNCH64(ST, BN)                                                                                   \
+  (out_dtype == kBF16 ? tile_gemm_dma_kernel<ST, BN, bf16_t, 2><<<grid, kDmaThreads, 0, stream>>>(MI355X_DMA_ARGS) \
+                      : tile_gemm_dma_kernel<ST, BN, f16_t, 2><<<grid, kDmaThreads, 0, stream>>>(MI355X_DMA_ARGS))
+  if (rows == 64) {
+    // 64-row tiles (half the activation rows of a tile, J = 2): for row counts just past a
+    // multiple of 64 whose 128-row tiles leave CUs idle.  Two workgroups per CU share it when
+    // the tiles outnumber the CUs.
+    if (!few) {
+      if (bn == 64) MI355X_DMA_LAUNCH64(MI355X_DMA_STAGES_MANY, 64);
+      else MI355X_DMA_LAUNCH64(MI355X_DMA_STAGES_MANY, 128);
+    } else {
+      if (bn == 64) MI355X_DMA_LAUNCH64(MI355X_DMA_STAGES_FEW_NARROW, 64);
+      else MI355X_DMA_LAUNCH64(MI355X_DMA_STAGES_FEW, 128);
+    }
+  } else if (!few) {
     if (bn == 160) MI355X_DMA_LAUNCH(MI355X_DMA_STAGES_MANY, 160);
     else if (bn == 64) MI355X_DMA_LAUNCH(MI355X_DMA_STAGES_MANY, 64);
     else MI355X_DMA_LAUNCH(MI355X_DMA_STAGES_MANY, 128);
@@ -475,6 +496,7 @@ int launch_tile_dma(const uint8_t* q, int64_t ldq, const float* as, int64_t as_s
     else if (bn == 64) MI355X_DMA_LAUNCH(MI355X_DMA_STAGES_FEW_NARROW, 64);
     else MI355X_DMA_LAUNCH(MI355X_DMA_STAGES_FEW, 128);
   }
+#undef MI355X_DMA_LAUNCH64
 #undef MI355X_DMA_LAUNCH
 #undef MI355X_DMA_ARGS
   return hipGetLastError() == hipSuccess ? MI355X_FP8_OK : MI355X_FP8_ERR_LAUNCH;

@@ -30,6 +30,7 @@ CONFIG_TILE256 = 3
 CONFIG_DMA128_64, CONFIG_DMA128_128, CONFIG_DMA128_160 = 4, 5, 6
 CONFIG_T256_128, CONFIG_T256_160, CONFIG_T256_192, CONFIG_T256_224, CONFIG_T256_256 = 7, 8, 9, 10, 11
 CONFIG_T192_128, CONFIG_T192_160, CONFIG_T192_192, CONFIG_T192_224, CONFIG_T192_256 = 12, 13, 14, 15, 16
+CONFIG_DMA64_64, CONFIG_DMA64_128 = 17, 18
 OK = 0
 ERR_INVALID = 1
 ERR_UNSUPPORTED = 2

@@ -77,6 +77,8 @@ GEMM_CONFIGS = (
     FP8GemmConfig("t192x192", _lib.CONFIG_T192_192, 192, 192),
     FP8GemmConfig("t192x224", _lib.CONFIG_T192_224, 192, 224),
     FP8GemmConfig("t192x256", _lib.CONFIG_T192_256, 192, 256),
+    FP8GemmConfig("dma64x64", _lib.CONFIG_DMA64_64, 64, 64),
+    FP8GemmConfig("dma64x128", _lib.CONFIG_DMA64_128, 64, 128),
 )
 # Alias under the reference's name.
 SPLIT_GEMM_CONFIGS = GEMM_CONFIGS

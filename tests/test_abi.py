@@ -45,6 +45,8 @@ def test_header_constants_match_binding():
                          "MI355X_FP8_CONFIG_T256_256": _lib.CONFIG_T256_256,
                          "MI355X_FP8_CONFIG_T192_128": _lib.CONFIG_T192_128,
                          "MI355X_FP8_CONFIG_T192_256": _lib.CONFIG_T192_256,
+                         "MI355X_FP8_CONFIG_DMA64_64": _lib.CONFIG_DMA64_64,
+                         "MI355X_FP8_CONFIG_DMA64_128": _lib.CONFIG_DMA64_128,
                          "MI355X_FP8_ABI_VERSION": _lib.ABI_VERSION}.items():
         assert re.search(rf"#define {macro} {value}\b", text), macro
 
@@ -87,7 +89,7 @@ def test_argument_validation_happens_before_any_launch():
     assert lib.mi355x_fp8_block_gemm(null, 64, null, 1, 1, null, 128, null, 1, 1, null, 0, 64, 4, 64, 128,
                                      null, 0, 0, null) == _lib.ERR_INVALID   # ldq < K
     assert lib.mi355x_fp8_block_gemm(null, 128, null, 1, 1, null, 128, null, 1, 1, null, 0, 64, 4, 64, 128,
-                                     null, 0, 17, null) == _lib.ERR_INVALID  # unknown config
+                                     null, 0, 19, null) == _lib.ERR_INVALID  # unknown config
     # The linear refuses a missing workspace before launching anything.
     dummy = ctypes.c_void_p(16)
     assert lib.mi355x_fp8_linear(dummy, 0, 4, 128, 128, 1, dummy, 128, dummy, 1, 1, 64, dummy, 0, 64, null, 0, 0,

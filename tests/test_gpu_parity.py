@@ -344,6 +344,9 @@ def test_prefill_2048_full_size(gpu, shape):
     (536, 19456, 256),    # 192x256 tiles (3 x 192 rows against 3 x 256)
     (320, 19456, 256),    # 192x160 tiles
     (864, 6144, 256),     # 192x128 tiles
+    (300, 2560, 384),     # 64x64 tiles (two per CU)
+    (300, 6144, 256),     # 64x128 tiles
+    (97, 200, 256),       # 64x64 tiles, row and column tails
     # Ring depth: three stages when the tiles fit within the CUs, two otherwise; K of 1 to
     # 5 groups exercises the prologue and the unrolled loop's tail at both depths.
     (300, 200, 128),      # 3 stages, one K group

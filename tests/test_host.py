@@ -44,7 +44,7 @@ def test_gemm_config_contract():
     configs = fp8.GEMM_CONFIGS
     assert len(set(configs)) == len(configs) and fp8.SPLIT_GEMM_CONFIGS is configs
     assert {c.name for c in configs} >= {"stream", "tile128", "tile256"}
-    assert [c.kernel for c in configs] == list(range(1, 17))  # every C-ABI config code, once
+    assert [c.kernel for c in configs] == list(range(1, 19))  # every C-ABI config code, once
     assert [c.name for c in configs if not c.needs_dma] == ["stream", "tile128"]
     for config in configs:
         assert config.block_k == 128
