@@ -146,6 +146,15 @@ int mi355x_fp8_linear_noalloc(const void* x, int x_dtype, int64_t M, int64_t K, 
 size_t mi355x_fp8_linear_noalloc_scratch_bytes(void);
 
 /*
+ * Dispatch introspection, no reference counterpart (for tests and tuning): the prefill
+ * kernel the automatic dispatch runs for an M x N output (M above the decode range, LDS-DMA
+ * preconditions met) on a device with `cus` CUs, from the table of measured wave times:
+ * *rows = tile rows (64 or 128: the LDS-DMA kernel; 192 or 256: the 256-row kernel and its
+ * 192-row form), *bn = tile width.  Pure host computation: no device is touched.
+ */
+int mi355x_fp8_prefill_choice(int64_t M, int64_t N, int64_t cus, int* rows, int* bn);
+
+/*
  * Measurement helper, no reference counterpart: reads `bytes` of device memory at `src`
  * once (16-byte loads over all CUs) and nothing else, so that a benchmark can time the
  * streaming-read rate one launch reaches over the same bytes as a decode GEMM.  bytes must

@@ -200,6 +200,12 @@ int mi355x_fp8_read_probe(const void* src, size_t bytes, void* sink, size_t sink
 
 size_t mi355x_fp8_linear_noalloc_scratch_bytes(void) { return MI355X_FP8_NOALLOC_SCRATCH_BYTES; }
 
+int mi355x_fp8_prefill_choice(int64_t M, int64_t N, int64_t cus, int* rows, int* bn) {
+  if (M <= 0 || N <= 0 || cus <= 0 || rows == nullptr || bn == nullptr) return MI355X_FP8_ERR_INVALID;
+  prefill_choice(M, N, cus, rows, bn);
+  return MI355X_FP8_OK;
+}
+
 int mi355x_fp8_linear_noalloc(const void* x, int x_dtype, int64_t M, int64_t K, int64_t sxm, int64_t sxk,
                               const uint8_t* w, int64_t ldw, const float* ws, int64_t ws_sn, int64_t ws_sk,
                               int64_t N, void* out, int out_dtype, int64_t ldo, int config, void* stream) {

@@ -798,7 +798,8 @@ int64_t device_cus() {
 // measured cases with the weights streamed from HBM (40 rotating sets, beyond the MALL), set
 // so that the model keeps the older variant where the two measured within 4 %, or where the
 // 64-row tile re-reads the weights from HBM more than it gains (64 x 128 for o_proj and down
-// at 536 and 700 rows, gate_up at 160 and 176, qkv at 1024); listed last, they lose ties.
+// at 536 and 700 rows, gate_up at 160 and 176); listed last, they lose ties.  (qkv at 1024
+// rows takes 192 x 160: 1-3 % either way against 256 x 128.)
 // A last, partly filled wave costs 0.7 + 0.3 x its fill of a full one (a half-filled wave
 // measured 0.75-0.98).  Every kernel gives the same bits, so the choice may follow M.
 #ifndef MI355X_PREFILL_POLICY
@@ -850,6 +851,12 @@ PrefillChoice choose_prefill(int64_t M, int64_t N, int64_t cus, bool rows256_ok)
   return best;
 }
 }  // namespace
+
+void prefill_choice(int64_t M, int64_t N, int64_t cus, int* rows, int* bn) {
+  const PrefillChoice c = choose_prefill(M, N, cus, true);
+  *rows = c.rows;
+  *bn = c.bn;
+}
 
 int tile256_width(int64_t M, int64_t N, int64_t cus) {
   int best = 256;

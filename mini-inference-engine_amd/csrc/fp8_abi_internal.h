@@ -72,6 +72,9 @@ int launch_tile256(const uint8_t* q, int64_t ldq, const float* as, int64_t as_sk
                    int64_t ldw, const float* ws, int64_t ws_sn, int64_t ws_sk, void* out, int out_dtype,
                    int64_t ldo, int64_t M, int64_t N, int64_t K, int bn, int rows, hipStream_t stream);
 int tile256_width(int64_t M, int64_t N, int64_t cus);
+// The prefill kernel the automatic dispatch picks for an M x N output on `cus` CUs (when the
+// LDS-DMA preconditions hold and the offsets fit): tile rows (64, 128, 192 or 256) and width.
+void prefill_choice(int64_t M, int64_t N, int64_t cus, int* rows, int* bn);
 // Whether the 256-row kernel's 32-bit byte offsets reach every byte of q and W.
 bool tile256_offsets_ok(int64_t ldq, int64_t ldw, int64_t M, int64_t N, int64_t K);
 

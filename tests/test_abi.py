@@ -102,3 +102,34 @@ def test_read_probe_validates_on_the_host():
     assert lib.mi355x_fp8_read_probe(None, 16, dummy, 4096, None) == _lib.ERR_INVALID
     assert lib.mi355x_fp8_read_probe(dummy, 15, dummy, 4096, None) == _lib.ERR_INVALID   # not whole 16-byte units
     assert lib.mi355x_fp8_read_probe(dummy, 0, dummy, 4096, None) == _lib.OK             # nothing to read
+
+
+# The automatic prefill dispatch's picks on 256 CUs (tile rows, tile width), from the table of
+# measured wave times in block_gemm.hip (choose_prefill): M -> (qkv, o_proj, gate_up, down).
+PREFILL_PICKS = {
+    96: [(64, 64), (64, 64), (128, 128), (64, 64)],
+    160: [(128, 64), (64, 64), (128, 160), (64, 64)],
+    300: [(64, 128), (64, 64), (192, 160), (64, 64)],
+    536: [(128, 128), (128, 64), (192, 256), (128, 64)],
+    864: [(192, 128), (128, 128), (128, 160), (128, 128)],
+    1024: [(192, 160), (128, 128), (256, 160), (128, 128)],
+    2048: [(256, 192), (128, 160), (256, 224), (128, 160)],
+    2208: [(256, 224), (192, 128), (256, 256), (192, 128)],
+    4096: [(256, 192), (256, 160), (256, 256), (256, 160)],
+}
+
+
+@pytest.mark.parametrize("m", sorted(PREFILL_PICKS))
+def test_prefill_dispatch_picks(m):
+    """The cost model's kernel for each Qwen3-4B projection (host computation only): the
+    M=2048 benchmark shapes, the 192-row tiles past multiples of 256 or 128 (config 5's 536
+    rows for gate_up), the 64-row tiles at small M."""
+
+    lib = _lib.load()
+    rows, bn = ctypes.c_int(), ctypes.c_int()
+    got = []
+    for n in (6144, 2560, 19456, 2560):
+        assert lib.mi355x_fp8_prefill_choice(m, n, 256, ctypes.byref(rows), ctypes.byref(bn)) == _lib.OK
+        got.append((rows.value, bn.value))
+    assert got == PREFILL_PICKS[m]
+    assert lib.mi355x_fp8_prefill_choice(0, 2560, 256, ctypes.byref(rows), ctypes.byref(bn)) == _lib.ERR_INVALID
