@@ -55,6 +55,9 @@ def parse_args(argv=None):
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--cpu-rows", type=int, default=4096)
     p.add_argument("--no-extras", action="store_true", help="skip the MLP-block and 36-layer-stack configs")
+    p.add_argument("--no-sweep", action="store_true", help="skip the M sweep (detail.sweep)")
+    p.add_argument("--sweep-ms", default="1,16,64,256,1024,2048,4096,8192,16384",
+                   help="row counts of the M sweep (the reference's benchmark range)")
     p.add_argument("--eager", action="store_true",
                    help="launch kernels directly instead of through HIP graphs (for counter collection)")
     p.add_argument("--only", choices=["prefill", "decode"], help="time one phase only")
@@ -217,6 +220,9 @@ def main(argv=None) -> int:
     if "decode" in results:
         print("timing the decode layer chain", file=sys.stderr, flush=True)
         results["decode"]["layer_chain"] = bench_decode_layers(torch, fp8, stream, args, weights, projs)
+    if not args.no_sweep:
+        print("timing the M sweep", file=sys.stderr, flush=True)
+        results["sweep"] = bench_sweep(torch, fp8, stream, args, weights, projs)
     del weights
     torch.cuda.empty_cache()
 
@@ -275,6 +281,62 @@ def main(argv=None) -> int:
     }
     print(json.dumps(line), flush=True)
     return 0
+
+
+def bench_sweep(torch, fp8, stream, args, weights, projs):
+    """GEMM-only and whole-linear (quantizer included) rate of each projection over the
+    reference's benchmark row counts (BENCH_MS, engine/kernels/sm89_fp8_validation.py:33),
+    so the dispatch crossovers show: per M, per projection, µs, TFLOPS and GB/s (op-level
+    bytes), and the kernel the dispatch picked.  Weights rotate through the same sets as the
+    headline phases; steps shrink with M so the sweep stays within a minute."""
+
+    from minillm_amd.validation import gemm_bytes, linear_flops, make_baseline_activations
+
+    lib = fp8._lib.load()
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    sets = len(weights)
+    out = {}
+    for m in (int(v) for v in args.sweep_ms.split(",") if v):
+        steps = max(2, min(args.steps, (args.steps * 256) // max(m, 256)))
+        row = {}
+        tot = {"gemm_us": 0.0, "linear_us": 0.0, "flops": 0, "bytes": 0}
+        for i, p in enumerate(projs):
+            x = make_baseline_activations(m, p.k, SEED + 17, outliers=m > 64, device="cuda")
+            q, s = fp8.quantize_mi355x_fp8_activation(x, scale_layout="kgroup")
+            o = torch.empty((m, p.n), dtype=torch.bfloat16, device="cuda")
+
+            def gemms(i=i, q=q, s=s, o=o):
+                for r in range(sets):
+                    fp8.launch_block_gemm(q, weights[r][i][0], o, s, weights[r][i][1])
+
+            def linears(i=i, x=x):
+                for r in range(sets):
+                    fp8.mi355x_fp8_linear(x, weights[r][i][0], weights[r][i][1], [128, 128])
+
+            g_ms = timed_graph(torch, stream, gemms, sets, steps, 1, args.eager)
+            l_ms = timed_graph(torch, stream, linears, sets, steps, 1, args.eager)
+            flops, nbytes = linear_flops(m, p.n, p.k), gemm_bytes(m, p.n, p.k)
+            kernel = fp8.dispatch_name(m, p.n, p.k, cus)
+            row[p.name] = {"kernel": kernel, "gemm_us": round(g_ms * 1e3, 2), "linear_us": round(l_ms * 1e3, 2),
+                           "gemm_tflops": round(flops / (g_ms * 1e9), 1),
+                           "linear_tflops": round(flops / (l_ms * 1e9), 1),
+                           "gemm_gbps": round(nbytes / (g_ms * 1e6), 1),
+                           "linear_gbps": round(nbytes / (l_ms * 1e6), 1)}
+            tot["gemm_us"] += g_ms * 1e3
+            tot["linear_us"] += l_ms * 1e3
+            tot["flops"] += flops
+            tot["bytes"] += nbytes
+            del x, q, s, o
+        row["all"] = {"gemm_us": round(tot["gemm_us"], 2), "linear_us": round(tot["linear_us"], 2),
+                      "gemm_tflops": round(tot["flops"] / (tot["gemm_us"] * 1e6), 1),
+                      "linear_tflops": round(tot["flops"] / (tot["linear_us"] * 1e6), 1),
+                      "gemm_gbps": round(tot["bytes"] / (tot["gemm_us"] * 1e3), 1),
+                      "linear_gbps": round(tot["bytes"] / (tot["linear_us"] * 1e3), 1)}
+        out[str(m)] = row
+        print(f"  sweep M={m}: GEMM {row['all']['gemm_tflops']} TFLOPS, linear {row['all']['linear_tflops']} TFLOPS",
+              file=sys.stderr, flush=True)
+        torch.cuda.empty_cache()
+    return out
 
 
 def bench_decode_layers(torch, fp8, stream, args, weights, projs):
@@ -370,12 +432,43 @@ def bench_stack(torch, fp8, stream, args, make_w, make_x, projs):
     ms = timed_graph(torch, stream, step, 1, max(2, args.steps // 4), 2, args.eager)
     flops = layers * sum(2 * m * p.n * p.k for p in projs)
     nbytes = layers * sum(p.n * p.k for p in projs)
+
+    # Per projection, over the same 36 independent weight sets: the GEMM on pre-quantized
+    # activations, the quantizer alone, and the whole linear (what the stack runs).
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    per_proj = {}
+    for i, p in enumerate(projs):
+        q, s = fp8.quantize_mi355x_fp8_activation(xs[i], scale_layout="kgroup")
+        o = torch.empty((m, p.n), dtype=torch.bfloat16, device="cuda")
+
+        def gemms(i=i, q=q, s=s, o=o):
+            for layer in range(layers):
+                fp8.launch_block_gemm(q, weights[layer][i][0], o, s, weights[layer][i][1])
+
+        def quants(i=i):
+            for _ in range(layers):
+                fp8.quantize_mi355x_fp8_activation(xs[i], scale_layout="kgroup")
+
+        def linears(i=i):
+            for layer in range(layers):
+                fp8.mi355x_fp8_linear(xs[i], weights[layer][i][0], weights[layer][i][1], [128, 128])
+
+        steps = max(2, args.steps // 4)
+        g = timed_graph(torch, stream, gemms, layers, steps, 1, args.eager)
+        qt = timed_graph(torch, stream, quants, layers, steps, 1, args.eager)
+        ln = timed_graph(torch, stream, linears, layers, steps, 1, args.eager)
+        f = 2 * m * p.n * p.k
+        per_proj[p.name] = {"kernel": fp8.dispatch_name(m, p.n, p.k, cus), "gemm_us": round(g * 1e3, 2),
+                            "quant_us": round(qt * 1e3, 2), "linear_us": round(ln * 1e3, 2),
+                            "gemm_tflops": round(f / (g * 1e9), 1),
+                            "gemm_frac_of_fp8_peak": round(f / (g * 1e9) / PEAK_FP8_TFLOPS, 4)}
     del weights
     torch.cuda.empty_cache()
     return {"config": "36-layer linear stack, 144 linears (quantizer + GEMM), M=536, independent weights",
             "ms": round(ms, 3), "tflops": round(flops / (ms * 1e9), 1),
             "weight_gbps": round(nbytes / (ms * 1e6), 1),
-            "frac_of_fp8_peak": round(flops / (ms * 1e9) / PEAK_FP8_TFLOPS, 4)}
+            "frac_of_fp8_peak": round(flops / (ms * 1e9) / PEAK_FP8_TFLOPS, 4),
+            "per_proj": per_proj}
 
 
 def cpu_baseline(rows: int) -> dict:

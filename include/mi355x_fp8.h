@@ -136,13 +136,17 @@ int mi355x_fp8_linear(const void* x, int x_dtype, int64_t M, int64_t K, int64_t 
  * MI355X_FP8_ERR_SCRATCH before launching anything.  The call allocates nothing and gives
  * the bits of mi355x_fp8_linear.  Every call on one GPU shares that GPU's scratch:
  * calls that overlap in time on one GPU (different streams, or host threads) race.
+ * Set-up: call mi355x_fp8_linear_noalloc_scratch_bytes() once per device, with that device
+ * current and outside graph capture; it looks up the device's scratch address (a
+ * hipGetSymbolAddress), which the first noalloc call on a device would otherwise do.
  */
 int mi355x_fp8_linear_noalloc(const void* x, int x_dtype, int64_t M, int64_t K, int64_t sxm,
                               int64_t sxk, const uint8_t* w, int64_t ldw, const float* ws,
                               int64_t ws_sn, int64_t ws_sk, int64_t N, void* out, int out_dtype,
                               int64_t ldo, int config, void* stream);
 
-/* MI355X_FP8_NOALLOC_SCRATCH_BYTES, as built into the library. */
+/* MI355X_FP8_NOALLOC_SCRATCH_BYTES, as built into the library; also resolves the current
+ * device's scratch address (the no-allocation entry point's set-up call). */
 size_t mi355x_fp8_linear_noalloc_scratch_bytes(void);
 
 /*
@@ -153,6 +157,16 @@ size_t mi355x_fp8_linear_noalloc_scratch_bytes(void);
  * 192-row form), *bn = tile width.  Pure host computation: no device is touched.
  */
 int mi355x_fp8_prefill_choice(int64_t M, int64_t N, int64_t cus, int* rows, int* bn);
+
+/*
+ * Dispatch introspection, no reference counterpart (for benchmarks and tests): the kernel
+ * family the automatic dispatch of an M x N x K GEMM picks on a device with `cus` CUs, for
+ * 16-byte aligned operands with K % 128 == 0.  *kernel = MI355X_FP8_CONFIG_STREAM (the
+ * weight-streaming decode kernel: *rows = weight rows per workgroup, *cols = token rows per
+ * slice) or MI355X_FP8_CONFIG_TILE128 (a prefill tile: *rows x *cols as in
+ * mi355x_fp8_prefill_choice).  Pure host computation: no device is touched.
+ */
+int mi355x_fp8_dispatch_choice(int64_t M, int64_t N, int64_t K, int64_t cus, int* kernel, int* rows, int* cols);
 
 /*
  * Measurement helper, no reference counterpart: reads `bytes` of device memory at `src`
@@ -214,7 +228,8 @@ int mi355x_fp8_rmsnorm_quant(const void* x, int x_dtype, int64_t M, int64_t K, i
  * (more than 8 rows, K not a multiple of 256 or above 2560, rows not 16-byte aligned, or a
  * shape the decode kernel does not take), and the caller then runs the two launches.
  * Operands as in mi355x_fp8_rmsnorm_quant (x, residual, norm weight) and mi355x_fp8_linear
- * (w, ws, out). */
+ * (w, ws, out).  residual_out must not overlap x or residual (every workgroup reads them
+ * while one writes the sum): such a call also returns MI355X_FP8_ERR_UNSUPPORTED. */
 int mi355x_fp8_rmsnorm_linear(const void* x, int64_t M, int64_t K, int64_t sxm, const void* residual, int64_t ldr,
                               void* residual_out, int64_t ldro, const void* norm_weight, float eps, const uint8_t* w,
                               int64_t ldw, const float* ws, int64_t ws_sn, int64_t ws_sk, int64_t N, void* out,

@@ -19,6 +19,16 @@ int64_t cdiv64(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 bool valid_dtype(int d) { return d == MI355X_FP8_DTYPE_BF16 || d == MI355X_FP8_DTYPE_F16; }
 
+// Byte range [p, p + bytes) of rows x cols 2-byte elements at row stride ld (elements).
+bool overlaps(const void* a, int64_t rows_a, int64_t cols_a, int64_t ld_a, const void* b, int64_t rows_b,
+              int64_t cols_b, int64_t ld_b) {
+  if (a == nullptr || b == nullptr || rows_a <= 0 || rows_b <= 0) return false;
+  const uintptr_t a0 = reinterpret_cast<uintptr_t>(a), b0 = reinterpret_cast<uintptr_t>(b);
+  const uintptr_t a1 = a0 + 2 * static_cast<uintptr_t>((rows_a - 1) * ld_a + cols_a);
+  const uintptr_t b1 = b0 + 2 * static_cast<uintptr_t>((rows_b - 1) * ld_b + cols_b);
+  return a0 < b1 && b0 < a1;
+}
+
 // Layout of the linear's workspace: [GEMM workspace | q (M x Kpad) | a_s (KB x Mpad)].
 struct LinearLayout {
   GemmPlan plan;
@@ -126,6 +136,11 @@ int mi355x_fp8_rmsnorm_linear(const void* x, int64_t M, int64_t K, int64_t sxm, 
     return MI355X_FP8_ERR_INVALID;
   if (M == 0 || N == 0) return MI355X_FP8_ERR_UNSUPPORTED;  // nothing to fuse: the caller's two launches handle it
   if (!x || !norm_weight || !w || !ws || !out) return MI355X_FP8_ERR_INVALID;
+  // Every workgroup reads x and residual while one of them writes residual_out: the sum may
+  // not land on either input (the two-launch form, one workgroup per row, takes that case).
+  if (residual != nullptr &&
+      (overlaps(residual_out, M, K, ldro, x, M, K, sxm) || overlaps(residual_out, M, K, ldro, residual, M, K, ldr)))
+    return MI355X_FP8_ERR_UNSUPPORTED;
   GemmPlan plan;
   const int st = plan_gemm(M, N, K, MI355X_FP8_CONFIG_AUTO, &plan);
   if (st != MI355X_FP8_OK) return st;
@@ -198,11 +213,32 @@ int mi355x_fp8_read_probe(const void* src, size_t bytes, void* sink, size_t sink
   return launch_read_probe(src, bytes, sink, sink_words, static_cast<hipStream_t>(stream));
 }
 
-size_t mi355x_fp8_linear_noalloc_scratch_bytes(void) { return MI355X_FP8_NOALLOC_SCRATCH_BYTES; }
+size_t mi355x_fp8_linear_noalloc_scratch_bytes(void) {
+  // Also the set-up call of the no-allocation entry point: resolves the scratch address of
+  // the current device here, outside any graph capture the caller starts later.
+  (void)scratch_ptr();
+  return MI355X_FP8_NOALLOC_SCRATCH_BYTES;
+}
 
 int mi355x_fp8_prefill_choice(int64_t M, int64_t N, int64_t cus, int* rows, int* bn) {
   if (M <= 0 || N <= 0 || cus <= 0 || rows == nullptr || bn == nullptr) return MI355X_FP8_ERR_INVALID;
   prefill_choice(M, N, cus, rows, bn);
+  return MI355X_FP8_OK;
+}
+
+int mi355x_fp8_dispatch_choice(int64_t M, int64_t N, int64_t K, int64_t cus, int* kernel, int* rows, int* cols) {
+  if (M <= 0 || N <= 0 || K <= 0 || cus <= 0 || kernel == nullptr || rows == nullptr || cols == nullptr)
+    return MI355X_FP8_ERR_INVALID;
+  GemmPlan plan;
+  const int st = plan_gemm_on(M, N, K, MI355X_FP8_CONFIG_AUTO, cus, &plan);
+  if (st != MI355X_FP8_OK) return st;
+  *kernel = plan.kernel;
+  if (plan.kernel == MI355X_FP8_CONFIG_STREAM) {
+    *rows = plan.rows;
+    *cols = 16 * plan.token_tiles;
+  } else {
+    prefill_choice(M, N, cus, rows, cols);
+  }
   return MI355X_FP8_OK;
 }
 

@@ -711,7 +711,11 @@ __global__ __launch_bounds__(kThreads, 2) void tile_gemm_kernel(
 static int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 int plan_gemm(int64_t M, int64_t N, int64_t K, int config, GemmPlan* plan) {
-  if (M < 0 || N < 0 || K <= 0) return MI355X_FP8_ERR_INVALID;
+  return plan_gemm_on(M, N, K, config, device_cus(), plan);
+}
+
+int plan_gemm_on(int64_t M, int64_t N, int64_t K, int config, int64_t cus, GemmPlan* plan) {
+  if (M < 0 || N < 0 || K <= 0 || cus <= 0) return MI355X_FP8_ERR_INVALID;
   *plan = GemmPlan{};
   if (config == MI355X_FP8_CONFIG_AUTO) {
     // Every kernel gives the same bits, so this is a speed choice only.  The stream kernel
@@ -719,8 +723,7 @@ int plan_gemm(int64_t M, int64_t N, int64_t K, int config, GemmPlan* plan) {
     // lead only while the weight rows give few workgroups (measured on the Qwen3-4B
     // shapes: at 64 rows o_proj / down 15 / 30 us streamed against 18 / 38 us tiled, qkv /
     // gate_up 20 / 50 us against 13 / 22 us; at 32 rows gate_up 24 against 22 us).
-    const bool stream = M <= 16 || (M <= 64 && cdiv(N, 16) <= device_cus()) ||
-                        (M <= 32 && cdiv(N, 16) <= 2 * device_cus());
+    const bool stream = M <= 16 || (M <= 64 && cdiv(N, 16) <= cus) || (M <= 32 && cdiv(N, 16) <= 2 * cus);
     config = stream ? MI355X_FP8_CONFIG_STREAM : MI355X_FP8_CONFIG_TILE128;
   }
   if (config < MI355X_FP8_CONFIG_STREAM || config > MI355X_FP8_CONFIG_DMA64_128) return MI355X_FP8_ERR_INVALID;
@@ -752,7 +755,7 @@ int plan_gemm(int64_t M, int64_t N, int64_t K, int config, GemmPlan* plan) {
   // workgroup, so that narrow weights do not spread over workgroups for a few rows each.
   {
     const int64_t slices = M > 0 ? cdiv(M, 16 * plan->token_tiles) : 1;
-    const int64_t cus = device_cus(), share = cus / slices > 1 ? cus / slices : 1;
+    const int64_t share = cus / slices > 1 ? cus / slices : 1;
     const int64_t rows = cdiv(N, share) > kStreamMinRows ? cdiv(N, share) : kStreamMinRows;
     const int64_t af = cdiv(rows, 16);
     const int64_t old_wgs = cdiv(N, plan->rows) * slices;
@@ -802,9 +805,6 @@ int64_t device_cus() {
 // rows takes 192 x 160: 1-3 % either way against 256 x 128.)
 // A last, partly filled wave costs 0.7 + 0.3 x its fill of a full one (a half-filled wave
 // measured 0.75-0.98).  Every kernel gives the same bits, so the choice may follow M.
-#ifndef MI355X_PREFILL_POLICY
-#define MI355X_PREFILL_POLICY 0  // 0: cost model, 1: always 256-row, 2: always 128-row
-#endif
 namespace {
 struct TileVariant {
   int rows, bn;
@@ -840,7 +840,6 @@ PrefillChoice choose_prefill(int64_t M, int64_t N, int64_t cus, bool rows256_ok)
   PrefillChoice best{128, 128};
   double best_cost = -1.0;
   for (const TileVariant& v : kTileVariants) {
-    if ((MI355X_PREFILL_POLICY == 1 && v.rows != 256) || (MI355X_PREFILL_POLICY == 2 && v.rows != 128)) continue;
     if (v.rows > 128 && !rows256_ok) continue;
     const double cost = variant_cost(v, M, N, cus);
     if (best_cost < 0.0 || cost < best_cost) {
@@ -1123,7 +1122,6 @@ int launch_linear_stream(const GemmPlan& plan, const void* x, int x_dtype, int64
       plan.rows < 1 || sxk != 1 || sxm % 8 != 0 || K % 16 != 0 || ldw % 16 != 0 ||
       reinterpret_cast<uintptr_t>(x) % 16 != 0 || reinterpret_cast<uintptr_t>(w) % 16 != 0)
     return MI355X_FP8_ERR_UNSUPPORTED;
-#ifndef MI355X_LINEAR_ALWAYS_ONE_LAUNCH
   // Every workgroup reads and quantizes all of x, about 7 VALU instructions per element of
   // x: the quantization pays only while it hides behind the workgroup's own weight loads.
   // Up to 8 rows (the lane-dense quantization passes) that holds for every Qwen3-4B
@@ -1135,7 +1133,6 @@ int launch_linear_stream(const GemmPlan& plan, const void* x, int x_dtype, int64
   // 14.6 -> 18.5 us, o_proj 9.4 -> 9.9 us).
   const int64_t kgroups = cdiv(K, kGroup);
   if (M <= 8 ? kgroups > 80 : (2 * M > plan.rows || kgroups > 24)) return MI355X_FP8_ERR_UNSUPPORTED;
-#endif
   uint16_t* o = static_cast<uint16_t*>(out);
   if (x_dtype == kBF16)
     return out_dtype == kBF16

@@ -33,6 +33,8 @@ struct GemmPlan {
 };
 
 int plan_gemm(int64_t M, int64_t N, int64_t K, int config, GemmPlan* plan);
+// The same plan for a device with `cus` compute units (plan_gemm: the current device's).
+int plan_gemm_on(int64_t M, int64_t N, int64_t K, int config, int64_t cus, GemmPlan* plan);
 
 // Device workspace the GEMM needs (none: every reduction stays inside a workgroup).
 size_t gemm_workspace_bytes(const GemmPlan& plan);

@@ -58,6 +58,8 @@ EXPORTS = {
     "mi355x_fp8_linear_noalloc_scratch_bytes": ([], _size),
     "mi355x_fp8_read_probe": ([_ptr, _size, _ptr, _size, _ptr], _int),
     "mi355x_fp8_prefill_choice": ([_i64, _i64, _i64, ctypes.POINTER(_int), ctypes.POINTER(_int)], _int),
+    "mi355x_fp8_dispatch_choice": ([_i64, _i64, _i64, _i64, ctypes.POINTER(_int), ctypes.POINTER(_int),
+                                    ctypes.POINTER(_int)], _int),
     "mi355x_fp8_linear": ([_ptr, _int, _i64, _i64, _i64, _i64, _ptr, _i64, _ptr, _i64, _i64, _i64, _ptr, _int,
                            _i64, _ptr, _size, _int, _ptr], _int),
 }

@@ -111,6 +111,20 @@ def pretune_row_buckets(max_tokens: int) -> tuple[int, ...]:
 _ARCH_OK: dict[int, bool] = {}  # device index -> is gfx950 (device properties do not change)
 
 
+def dispatch_name(rows: int, n: int, k: int, cus: int = 256) -> str:
+    """The kernel the automatic dispatch runs for an ``rows x n x k`` GEMM on ``cus`` CUs
+    (aligned operands, K % 128 == 0): ``"stream WxT"`` (the weight-streaming decode kernel,
+    W weight rows per workgroup, T token rows per slice) or ``"tile RxC"`` (a prefill tile).
+    Host-only: asks the library's planner, touches no device."""
+
+    import ctypes
+
+    kernel, r, c = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+    _lib.check(_lib.load().mi355x_fp8_dispatch_choice(rows, n, k, cus, ctypes.byref(kernel), ctypes.byref(r),
+                                                       ctypes.byref(c)))
+    return f"{'stream' if kernel.value == _lib.CONFIG_STREAM else 'tile'} {r.value}x{c.value}"
+
+
 def _device_index(device: torch.device | str | int | None) -> int:
     if device is None:
         return torch.cuda.current_device()

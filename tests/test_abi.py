@@ -133,3 +133,47 @@ def test_prefill_dispatch_picks(m):
         got.append((rows.value, bn.value))
     assert got == PREFILL_PICKS[m]
     assert lib.mi355x_fp8_prefill_choice(0, 2560, 256, ctypes.byref(rows), ctypes.byref(bn)) == _lib.ERR_INVALID
+
+
+def test_rmsnorm_linear_rejects_a_residual_sum_over_its_inputs():
+    """The one-launch norm-linear refuses residual_out overlapping x or residual (every
+    workgroup reads them while one writes the sum) before touching the device; a disjoint
+    sum passes that check (and then fails on the invalid stride, still host-side)."""
+
+    lib = _lib.load()
+    m, k, n = 4, 2560, 6144
+    x, res = 0x10000000, 0x20000000
+    ws, w, nw, out = 0x30000000, 0x40000000, 0x50000000, 0x60000000
+
+    def call(res_out, ldo=n):
+        return lib.mi355x_fp8_rmsnorm_linear(x, m, k, k, res, k, res_out, k, nw, 1e-6, w, k, ws, 20, 1, n, out,
+                                            ldo, None)
+
+    assert call(res) == _lib.ERR_UNSUPPORTED
+    assert call(x) == _lib.ERR_UNSUPPORTED
+    assert call(res + 2 * k * (m - 1)) == _lib.ERR_UNSUPPORTED  # last row of the residual
+    assert call(res - 2 * k * m + 2) == _lib.ERR_UNSUPPORTED   # ends one element inside it
+    assert call(res - 2 * k * m, ldo=n - 1) == _lib.ERR_INVALID  # adjacent, not overlapping
+
+
+def test_dispatch_choice_names_the_stream_kernel_then_the_prefill_tiles():
+    """The automatic dispatch's kernel family (host computation only): the weight-streaming
+    kernel at decode sizes (one 16-token slice up to 16 rows; 32-row slices above while the
+    weight rows give few workgroups), then the prefill tile the cost model picks (the same
+    as mi355x_fp8_prefill_choice)."""
+
+    from minillm_amd import mi355x_fp8 as fp8
+
+    shapes = ((6144, 2560), (2560, 4096), (19456, 2560), (2560, 9728))
+    for n, k in shapes:
+        for m in (1, 8, 16):
+            name = fp8.dispatch_name(m, n, k)
+            assert name.startswith("stream ") and name.endswith("x16"), (m, n, name)
+    assert [fp8.dispatch_name(32, n, k) for n, k in shapes] == [
+        "stream 24x32", "stream 10x32", "tile 64x128", "stream 16x32"]
+    for m in (160, 536, 2048):
+        assert [fp8.dispatch_name(m, n, k) for n, k in shapes] == [f"tile {r}x{c}" for r, c in PREFILL_PICKS[m]]
+    lib = _lib.load()
+    a, b, c = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+    assert lib.mi355x_fp8_dispatch_choice(0, 2560, 2560, 256, ctypes.byref(a), ctypes.byref(b),
+                                          ctypes.byref(c)) == _lib.ERR_INVALID

@@ -17,7 +17,7 @@ import pytest
 import torch
 
 import oracle
-from _helpers import assert_close_rows, bits16, codes, oracle_gemm, oracle_linear, oracle_quant
+from _helpers import assert_close_rows, bits16, record_parity, codes, oracle_gemm, oracle_linear, oracle_quant
 from minillm_amd import merged_projections as mp
 from minillm_amd import mi355x_fp8 as fp8
 from minillm_amd.validation import (
@@ -51,7 +51,7 @@ def test_config1_merged_qkv_m16(gpu, path):
     assert bitwise_equal(s.cpu(), s_ref), bit_mismatch_details(s.cpu(), s_ref)
     out = fp8.mi355x_fp8_linear(xg, wg, wsg, BLOCK, path=path)
     assert out.shape == (16, 6144) and out.dtype == torch.bfloat16
-    assert_close_rows(out, oracle_linear(x, w, ws))
+    record_parity(f"config1 qkv m16 {path}", assert_close_rows(out, oracle_linear(x, w, ws)))
     # The GEMM entry on the oracle's own codes and scales: same tolerance.
     gemm = torch.empty_like(out)
     fp8.launch_block_gemm(q_ref.to(gpu), wg, gemm, s_ref.to(gpu), wsg)
@@ -108,7 +108,7 @@ def test_config5_projection_m536(gpu, proj):
     q_ref, s_ref = oracle_quant(x)
     assert bitwise_equal(q.cpu(), q_ref) and bitwise_equal(s.cpu(), s_ref)
     out = fp8.mi355x_fp8_linear(xg, wg, wsg, BLOCK)
-    assert_close_rows(out, oracle_gemm(q_ref, s_ref, w, ws))
+    record_parity(f"config5 {proj} m536", assert_close_rows(out, oracle_gemm(q_ref, s_ref, w, ws)))
 
 
 def test_config5_two_layer_chain(gpu):
@@ -140,13 +140,14 @@ def test_config5_two_layer_chain(gpu):
         qkv = torch.empty((m, 6144), dtype=torch.bfloat16, device=gpu)
         fp8.launch_block_gemm(q, wsg["qkv"][0], qkv, s, wsg["qkv"][1])
         w, sc = ws_["qkv"]
-        assert_close_rows(qkv, _bf16(oracle.block_gemm(q_ref, s_ref, codes(w), sc.numpy())))
+        record_parity(f"config5 chain{layer} qkv", assert_close_rows(qkv, _bf16(oracle.block_gemm(q_ref, s_ref, codes(w), sc.numpy()))))
 
         # attention is outside this path: its stand-in output is the q columns (K = 4096)
         attn = qkv[:, :4096]
         o = fp8.mi355x_fp8_linear(attn, *wsg["o_proj"], BLOCK)
         w, sc = ws_["o_proj"]
-        assert_close_rows(o, _bf16(oracle.linear(bits16(attn), codes(w), sc.numpy())))
+        record_parity(f"config5 chain{layer} o_proj",
+                      assert_close_rows(o, _bf16(oracle.linear(bits16(attn), codes(w), sc.numpy()))))
 
         # post-attention norm with the residual -> gate_up -> SiLU*up + requant -> down
         y2, q2, s2, summed2 = fp8.rmsnorm_quant_mi355x_fp8(o, norm2.to(gpu), eps, summed, scale_layout="row",
@@ -158,7 +159,8 @@ def test_config5_two_layer_chain(gpu):
         gate_up = torch.empty((m, 2 * inter), dtype=torch.bfloat16, device=gpu)
         fp8.launch_block_gemm(q2, wsg["gate_up"][0], gate_up, s2, wsg["gate_up"][1])
         w, sc = ws_["gate_up"]
-        assert_close_rows(gate_up, _bf16(oracle.block_gemm(q2_ref, s2_ref, codes(w), sc.numpy())))
+        record_parity(f"config5 chain{layer} gate_up",
+                      assert_close_rows(gate_up, _bf16(oracle.block_gemm(q2_ref, s2_ref, codes(w), sc.numpy()))))
 
         hmid, q3, s3 = fp8.silu_mul_quant_mi355x_fp8(gate_up[:, :inter], gate_up[:, inter:], scale_layout="row",
                                                      return_intermediate=True)
@@ -170,7 +172,8 @@ def test_config5_two_layer_chain(gpu):
         down = torch.empty((m, hidden), dtype=torch.bfloat16, device=gpu)
         fp8.launch_block_gemm(q3, wsg["down"][0], down, s3, wsg["down"][1])
         w, sc = ws_["down"]
-        assert_close_rows(down, _bf16(oracle.block_gemm(q3_ref, s3_ref, codes(w), sc.numpy())))
+        record_parity(f"config5 chain{layer} down",
+                      assert_close_rows(down, _bf16(oracle.block_gemm(q3_ref, s3_ref, codes(w), sc.numpy()))))
 
         hg, rg = down, summed2
     assert torch.isfinite(hg.float()).all()

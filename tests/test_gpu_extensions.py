@@ -9,7 +9,7 @@ import pytest
 import torch
 
 import oracle
-from _helpers import assert_close_rows, bits16, codes, crafted_sumsq_rows, oracle_linear, sumsq_eps_sweep
+from _helpers import assert_close_rows, record_parity, bits16, codes, crafted_sumsq_rows, oracle_linear, sumsq_eps_sweep
 from minillm_amd import _lib
 from minillm_amd import merged_projections as mp
 from minillm_amd import mi355x_fp8 as fp8
@@ -74,12 +74,12 @@ def test_mlp_block_config4(gpu, rows):
     out = fp8.mlp_forward_mi355x_fp8(xg, wgu.to(gpu), sgu.to(gpu), wd.to(gpu), sd.to(gpu))
     # Reference chain on the oracle, stage by stage, each against the GPU's intermediate.
     gate_up = fp8.mi355x_fp8_linear(xg, wgu.to(gpu), sgu.to(gpu), [128, 128])
-    assert_close_rows(gate_up, oracle_linear(x, wgu, sgu))
+    record_parity(f"config4 gate_up m{rows}", assert_close_rows(gate_up, oracle_linear(x, wgu, sgu)))
     h, q, s = fp8.silu_mul_quant_mi355x_fp8(gate_up[:, :9728], gate_up[:, 9728:], return_intermediate=True)
     q_ref, s_ref = oracle.act_quant(bits16(h))
     assert np.array_equal(codes(q), q_ref)
     down_ref = oracle.block_gemm(q_ref, s_ref, codes(wd), sd.numpy())
-    assert_close_rows(out, _bf16(down_ref))
+    record_parity(f"config4 down m{rows}", assert_close_rows(out, _bf16(down_ref)))
 
 
 @pytest.mark.parametrize("rows", [1, 8, 100, 300, 2048])

@@ -10,7 +10,7 @@ import sys
 import pytest
 import torch
 
-from _helpers import assert_close_rows, oracle_gemm, oracle_linear, oracle_quant
+from _helpers import assert_close_rows, oracle_gemm, oracle_linear, oracle_quant, record_parity
 from minillm_amd import mi355x_fp8 as fp8
 from minillm_amd.validation import (
     MODEL_SHAPES, QWEN3_4B_PROJECTIONS, SEED, TAIL_SHAPES, ModelShape, bit_mismatch_details,
@@ -292,7 +292,7 @@ def test_decode_shapes_baseline_data(gpu, shape, rows):
     x = make_baseline_activations(rows, shape.k, SEED)
     w, ws = baseline_weights(shape)
     out = fp8.mi355x_fp8_linear(x.to(gpu), w.to(gpu), ws.to(gpu), BLOCK)
-    assert_close_rows(out, oracle_linear(x, w, ws))
+    record_parity(f"config2 {shape.name} m{rows}", assert_close_rows(out, oracle_linear(x, w, ws)))
 
 
 def _dense(x, w, ws, n, k):
@@ -328,7 +328,7 @@ def test_prefill_2048_full_size(gpu, shape):
     assert_close_rows(out, _dense(a_deq, wg, wsg, shape.n, shape.k))
     sample = [0, 1, 2, 511, 1024, 2047]
     expected = oracle_linear(x[sample], w, ws)
-    assert_close_rows(out[sample], expected)
+    record_parity(f"config3 {shape.name} m2048 (sampled rows)", assert_close_rows(out[sample], expected))
     dense = _dense(xg[sample], wg, wsg, shape.n, shape.k)
     ours, oracle_err = _rel_l2(out[sample], dense), _rel_l2(expected.to(gpu), dense)
     assert (ours <= 1.25 * oracle_err + 1e-4).all(), (ours.tolist(), oracle_err.tolist())
