@@ -343,10 +343,10 @@ def bench_decode_layers(torch, fp8, stream, args, weights, projs):
     """The decode linears as a model runs them, chained over the rotating weight sets (one
     set per layer): residual add + RMSNorm + quantizer -> qkv GEMM; the q columns (the
     attention stand-in) -> quantizer + o_proj GEMM; residual add + RMSNorm + quantizer ->
-    gate_up GEMM; SiLU*up + quantizer -> down GEMM.  Five launches per layer up to 8 rows
-    (the two norms, their quantizers and the o_proj quantizer run inside the GEMM launches),
-    eight above; none of them a standalone quantizer in front of qkv, gate_up or down.
-    Reported: time per layer and the layer's weight bytes per second."""
+    gate_up GEMM -> SiLU*up; quantizer -> down GEMM.  Four launches per layer up to 8 rows
+    (the two norms, every quantizer and the SiLU*up run inside the GEMM launches), eight
+    above.  Reported: time per layer and the layer's weight bytes per second, and the same
+    chain with SiLU*up + quantizer as a launch of its own."""
 
     m, hidden, eps = args.decode_m, 2560, 1e-6
     gen = torch.Generator().manual_seed(SEED + 3)
@@ -362,15 +362,27 @@ def bench_decode_layers(torch, fp8, stream, args, weights, projs):
         for (qkv_w, o_w, gu_w, d_w), (n1, n2) in zip(weights, norms):
             qkv, summed = fp8.rmsnorm_linear_mi355x_fp8(h, n1, eps, qkv_w[0], qkv_w[1], residual=res)
             o = fp8.mi355x_fp8_linear(qkv[:, :projs[1].k], o_w[0], o_w[1], [128, 128])
+            act, res = fp8.rmsnorm_gate_up_silu_mi355x_fp8(o, n2, eps, gu_w[0], gu_w[1], residual=summed)
+            h = fp8.mi355x_fp8_linear(act, d_w[0], d_w[1], [128, 128])
+
+    def chain_separate():
+        # The same layer with the SiLU*up + quantizer as its own launch after the gate_up
+        # norm-linear, the down GEMM on its codes (the form before the gate_up/SiLU fusion).
+        h, res = h0, r0
+        for (qkv_w, o_w, gu_w, d_w), (n1, n2) in zip(weights, norms):
+            qkv, summed = fp8.rmsnorm_linear_mi355x_fp8(h, n1, eps, qkv_w[0], qkv_w[1], residual=res)
+            o = fp8.mi355x_fp8_linear(qkv[:, :projs[1].k], o_w[0], o_w[1], [128, 128])
             gu, res = fp8.rmsnorm_linear_mi355x_fp8(o, n2, eps, gu_w[0], gu_w[1], residual=summed)
             q3, s3 = fp8.silu_mul_quant_mi355x_fp8(gu[:, :inter], gu[:, inter:])
             fp8.launch_block_gemm(q3, d_w[0], out, s3, d_w[1])
             h = out
 
     ms = timed_graph(torch, stream, chain, len(weights), args.steps, args.warmup, args.eager)
+    ms_sep = timed_graph(torch, stream, chain_separate, len(weights), args.steps, args.warmup, args.eager)
     nbytes = sum(p.n * p.k + 4 * ((p.n + 127) // 128) * ((p.k + 127) // 128) for p in projs)
     return {"us_per_layer": round(ms * 1e3, 2), "weight_gbps": round(nbytes / (ms * 1e6), 1),
-            "launches_per_layer": 5 if m <= 8 else 8}
+            "launches_per_layer": 4 if m <= 8 else 8,
+            "separate_silu_us_per_layer": round(ms_sep * 1e3, 2)}
 
 
 def bench_rmsnorm_quant(torch, fp8, stream, args):

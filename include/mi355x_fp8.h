@@ -235,6 +235,25 @@ int mi355x_fp8_rmsnorm_linear(const void* x, int64_t M, int64_t K, int64_t sxm, 
                               int64_t ldw, const float* ws, int64_t ws_sn, int64_t ws_sk, int64_t N, void* out,
                               int64_t ldo, void* stream);
 
+/* Residual add + RMSNorm + activation quantizer + merged gate/up block GEMM + SiLU*up in one
+ * launch, at decode sizes: h = silu_mul(fp8_linear(rms_norm(x [+ residual]), w)) with w the
+ * merged gate/up weight (N = 2 I rows, gate rows first, as merged_projections builds it) and
+ * h [M, I] bf16 (row stride ldh >= I).  It replaces the reference's rms_norm
+ * (engine/kernels/fused.py:165-199), the merged gate_up sm89_fp8_linear (engine/kernels/
+ * sm89_fp8.py:444-528, through merged_projections.project_gate_up) and silu_mul
+ * (fused.py:217-232, the _silu_mul_kernel of fused.py:127-137), and gives the bits of this
+ * library's separate forms: mi355x_fp8_rmsnorm_linear's gate_up output, then
+ * h = bf16(bf16(g / (1 + exp(-g))) * u) on its bf16 gate and up columns (the h of
+ * mi355x_fp8_silu_mul_quant).  residual_out receives bf16(x + residual).  Each workgroup owns
+ * matching gate and up rows; it returns MI355X_FP8_ERR_UNSUPPORTED, having launched nothing,
+ * under the conditions of mi355x_fp8_rmsnorm_linear (more than 8 rows, K not a multiple of
+ * 256 or above 2560, unaligned rows, residual_out over an input) or when N is odd, and the
+ * caller then runs the separate launches.  Operands as in mi355x_fp8_rmsnorm_linear. */
+int mi355x_fp8_rmsnorm_gate_up_silu(const void* x, int64_t M, int64_t K, int64_t sxm, const void* residual,
+                                    int64_t ldr, void* residual_out, int64_t ldro, const void* norm_weight, float eps,
+                                    const uint8_t* w, int64_t ldw, const float* ws, int64_t ws_sn, int64_t ws_sk,
+                                    int64_t N, void* h, int64_t ldh, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

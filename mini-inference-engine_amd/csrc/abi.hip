@@ -150,6 +150,24 @@ int mi355x_fp8_rmsnorm_linear(const void* x, int64_t M, int64_t K, int64_t sxm, 
                             static_cast<hipStream_t>(stream));
 }
 
+int mi355x_fp8_rmsnorm_gate_up_silu(const void* x, int64_t M, int64_t K, int64_t sxm, const void* residual,
+                                    int64_t ldr, void* residual_out, int64_t ldro, const void* norm_weight, float eps,
+                                    const uint8_t* w, int64_t ldw, const float* ws, int64_t ws_sn, int64_t ws_sk,
+                                    int64_t N, void* h, int64_t ldh, void* stream) {
+  if (M < 0 || N < 0 || N % 2 != 0 || K < 128 || K % 4 != 0 || sxm < K || ldw < K || ldh < N / 2 ||
+      (residual != nullptr && (ldr < K || residual_out == nullptr || ldro < K)))
+    return MI355X_FP8_ERR_INVALID;
+  if (M == 0 || N == 0) return MI355X_FP8_ERR_UNSUPPORTED;
+  if (!x || !norm_weight || !w || !ws || !h) return MI355X_FP8_ERR_INVALID;
+  if (residual != nullptr &&
+      (overlaps(residual_out, M, K, ldro, x, M, K, sxm) || overlaps(residual_out, M, K, ldro, residual, M, K, ldr)))
+    return MI355X_FP8_ERR_UNSUPPORTED;
+  return launch_norm_gate_up_silu(static_cast<const uint16_t*>(x), sxm, static_cast<const uint16_t*>(residual), ldr,
+                                  static_cast<uint16_t*>(residual_out), ldro,
+                                  static_cast<const uint16_t*>(norm_weight), eps, w, ldw, ws, ws_sn, ws_sk,
+                                  static_cast<uint16_t*>(h), ldh, M, N, K, static_cast<hipStream_t>(stream));
+}
+
 size_t mi355x_fp8_block_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int config) {
   GemmPlan plan;
   if (plan_gemm(M, N, K, config, &plan) != MI355X_FP8_OK) return 0;

@@ -55,8 +55,10 @@ constexpr int64_t kStreamMinRows = 8;
 // LDS of the one-round fold: the raw partials [KB][16 nt][16 af] and, per K group and token,
 // the scale products with the `blocks` (one, or two for ragged row counts) 128-row
 // weight-scale blocks a workgroup's rows touch.
-__host__ __device__ constexpr size_t stream_fold_bytes(int64_t kb, int af, int nt, int blocks = 1) {
-  return static_cast<size_t>(kb) * (static_cast<size_t>(af) * nt * 256 + blocks * 16 * nt) * sizeof(float);
+__host__ __device__ constexpr size_t stream_fold_bytes(int64_t kb, int af, int nt, int blocks = 1, int tok_slots = 0) {
+  return static_cast<size_t>(kb) *
+         (static_cast<size_t>(af) * 16 * (tok_slots ? tok_slots : 16 * nt) + blocks * (tok_slots ? tok_slots : 16 * nt)) *
+         sizeof(float);
 }
 
 // The fold: the waves publish each K group's raw MFMA partials and the scale products
@@ -245,7 +247,7 @@ __device__ __forceinline__ float norm_row_inv(const uint2 (&xv)[kNormMaxVec], in
 }
 
 template <int NT, int AF, bool ALIGNED, bool RAGGED, typename OutT, typename XIn = uint8_t, int QT = 16,
-          bool NORM = false>
+          bool NORM = false, bool SILU = false>
 __global__ __launch_bounds__(kStreamWaves * 64) void stream_gemm_kernel(
     const uint8_t* __restrict__ q, int64_t ldq, const float* __restrict__ as, int64_t as_sm,
     int64_t as_sk, const uint8_t* __restrict__ w, int64_t ldw, const float* __restrict__ ws,
@@ -278,17 +280,28 @@ __global__ __launch_bounds__(kStreamWaves * 64) void stream_gemm_kernel(
   // GEMM.  Each workgroup repeats this for the (at most 8) rows: 8 K-element rows of work
   // against its own 16 AF K-element weight rows.
   static_assert(!NORM || (kDense && std::is_same<XIn, bf16_t>::value), "RMSNorm: bf16 rows, up to 8 tokens");
+  // SILU: the merged gate/up weight (N = 2 I rows, gate rows first) times the rows, then
+  // h = bf16(bf16(silu(gate)) * up) per column (the reference's silu_mul, engine/kernels/
+  // fused.py:127-137): a workgroup owns gate rows [n0, n0 + rows) and the up rows I + n0 ..,
+  // its first AF / 2 MFMA tiles the gate rows, the rest the up rows, so that one thread folds
+  // a column's gate and up outputs and writes h[.., n0 + j] (ldo, N / 2 columns).
+  static_assert(!SILU || (NORM && RAGGED && AF % 2 == 0), "SiLU epilogue: the norm form, paired row tiles");
   constexpr int kRows = 16 * AF;
   constexpr int kTok = 16 * NT;
-  constexpr int kSB = RAGGED ? 2 : 1;
+  // Token slots kept in the fold buffer: the norm form takes at most 8 rows, so only the MFMA
+  // tile's first 8 token columns are published.
+  constexpr int kTokS = NORM ? 8 : kTok;
+  constexpr int kSB = SILU ? 4 : (RAGGED ? 2 : 1);
+  constexpr int kHalfT = SILU ? AF / 2 : AF;  // MFMA tiles per row range
   const int rows = RAGGED ? rows_arg : kRows;
-  // [KB][kTok][kRows] partials, element-major (the fold's reads are consecutive), then
-  // [KB][kSB][kTok] scale products (first and last weight-scale block of the rows).
+  // [KB][kTokS][kRows] partials, element-major (the fold's reads are consecutive), then
+  // [KB][kSB][kTokS] scale products (first and last weight-scale block of the rows; with SILU
+  // those of the gate rows, then those of the up rows).
   float* part = reinterpret_cast<float*>(stream_fold_lds);
-  float* scl = part + KB * kTok * kRows;
+  float* scl = part + KB * kTokS * kRows;
   // NORM: the rows' 1 / rms [16], the norm weight [K] (bf16), then the rows' bf16(x + residual)
   // [M][K + 8] (rows four banks apart).
-  [[maybe_unused]] float* ninv = scl + KB * kSB * kTok;
+  [[maybe_unused]] float* ninv = scl + KB * kSB * kTokS;
   [[maybe_unused]] uint16_t* wl = reinterpret_cast<uint16_t*>(ninv + 16);
   [[maybe_unused]] const int64_t xpitch = K + 8;
   [[maybe_unused]] uint16_t* xs = wl + K;
@@ -298,12 +311,18 @@ __global__ __launch_bounds__(kStreamWaves * 64) void stream_gemm_kernel(
   const int lane = tid & 63;
   const int r = lane & 15;
   const int g = lane >> 4;
+  // SILU: rows index the gate half [0, N / 2); the up rows sit N / 2 further on.
+  const int64_t n_rows = SILU ? N / 2 : N;
   const int64_t n0 = static_cast<int64_t>(blockIdx.x) * rows;
-  const int64_t n_end = n0 + rows < N ? n0 + rows : N;
+  const int64_t n_end = n0 + rows < n_rows ? n0 + rows : n_rows;
   const int64_t m_base = static_cast<int64_t>(blockIdx.z) * kTok;
   const int64_t m_rows = (M - m_base) < kTok ? (M - m_base) : kTok;
   const int64_t nb0 = n0 / kGroup, nb1 = (n_end - 1) / kGroup;
+  [[maybe_unused]] const int64_t nbu0 = (n_rows + n0) / kGroup, nbu1 = (n_rows + n_end - 1) / kGroup;
   const int64_t wave_u = __builtin_amdgcn_readfirstlane(wave);
+  // First weight row of MFMA tile i and the end of its row range.
+  auto tile_row = [&](int i) -> int64_t { return i < kHalfT ? n0 + 16 * i : n_rows + n0 + 16 * (i - kHalfT); };
+  auto tile_end = [&](int i) -> int64_t { return RAGGED ? (i < kHalfT ? n_end : n_rows + n_end) : N; };
 
   // Operands of one K group in registers.  Waves keep two groups of loads in flight when
   // the workgroup holds up to three 16-row tiles of one token tile (two when quantizing),
@@ -356,12 +375,16 @@ __global__ __launch_bounds__(kStreamWaves * 64) void stream_gemm_kernel(
     }
 #pragma unroll
     for (int i = 0; i < AF; ++i) {
-      const int64_t row = n0 + 16 * i + r;
-      o.a[i] = pack_v8i(load_chunk16<ALIGNED>(w, ldw, row, RAGGED ? n_end : N, k_lo, K),
-                        load_chunk16<ALIGNED>(w, ldw, row, RAGGED ? n_end : N, k_lo + 64, K));
+      const int64_t row = tile_row(i) + r;
+      o.a[i] = pack_v8i(load_chunk16<ALIGNED>(w, ldw, row, tile_end(i), k_lo, K),
+                        load_chunk16<ALIGNED>(w, ldw, row, tile_end(i), k_lo + 64, K));
     }
     o.wsv[0] = ws[nb0 * ws_sn + kb * ws_sk];
-    if constexpr (RAGGED) o.wsv[kSB - 1] = ws[nb1 * ws_sn + kb * ws_sk];
+    if constexpr (RAGGED) o.wsv[1] = ws[nb1 * ws_sn + kb * ws_sk];
+    if constexpr (SILU) {
+      o.wsv[2] = ws[nbu0 * ws_sn + kb * ws_sk];
+      o.wsv[3] = ws[nbu1 * ws_sn + kb * ws_sk];
+    }
     if constexpr (!kQuant) {
 #pragma unroll
       for (int j = 0; j < NT; ++j) {
@@ -465,17 +488,19 @@ __global__ __launch_bounds__(kStreamWaves * 64) void stream_gemm_kernel(
       for (int j = 0; j < NT; ++j) sc[b][j] = o.asv[j] * o.wsv[b];
     if (kb_next < KB) load(o, kb_next);
     // Lane holds D[n = 16 i + 4 g + v][tok = 16 j + r]: four consecutive n of one token.
+    if (kTokS == kTok || r < kTokS) {
 #pragma unroll
-    for (int i = 0; i < AF; ++i)
+      for (int i = 0; i < AF; ++i)
 #pragma unroll
-      for (int j = 0; j < NT; ++j)
-        *reinterpret_cast<float4*>(part + (kb * kTok + 16 * j + r) * kRows + 16 * i + 4 * g) =
-            make_float4(p[i][j][0], p[i][j][1], p[i][j][2], p[i][j][3]);
-    if (g == 0) {
+        for (int j = 0; j < NT; ++j)
+          *reinterpret_cast<float4*>(part + (kb * kTokS + 16 * j + r) * kRows + 16 * i + 4 * g) =
+              make_float4(p[i][j][0], p[i][j][1], p[i][j][2], p[i][j][3]);
+      if (g == 0) {
 #pragma unroll
-      for (int b = 0; b < kSB; ++b)
+        for (int b = 0; b < kSB; ++b)
 #pragma unroll
-        for (int j = 0; j < NT; ++j) scl[(kb * kSB + b) * kTok + 16 * j + r] = sc[b][j];
+          for (int j = 0; j < NT; ++j) scl[(kb * kSB + b) * kTokS + 16 * j + r] = sc[b][j];
+      }
     }
   };
   constexpr int kDepth = ALIGNED && NT == 1 && AF <= (kQuant ? 2 : 3) ? 2 : 1;
@@ -546,27 +571,43 @@ __global__ __launch_bounds__(kStreamWaves * 64) void stream_gemm_kernel(
   }
   __syncthreads();
   // One output element (token, row) per thread, two when rows x tokens exceeds the threads.
-  const int live = RAGGED ? static_cast<int>(n_end - n0) : kRows;
-  for (int e = tid; e < live * kTok; e += kStreamWaves * 64) {
-    const int tok = e / live, nl = e - (e / live) * live;
-    if (tok >= m_rows) break;  // padding tokens: nothing to fold (later e only have larger tok)
-    const float* pf = part + tok * kRows + nl;
-    const float* sf = scl + (RAGGED && (n0 + nl) / kGroup != nb0 ? kTok : 0) + tok;
-    // Reads in batches of eight ahead of their FMAs, so the chain waits on LDS once per batch.
+  // The chain over the K groups in increasing order; reads in batches of eight ahead of their
+  // FMAs, so the chain waits on LDS once per batch.
+  auto fold = [&](const float* pf, const float* sf) {
     float acc = 0.0f;
     int64_t kb = 0;
     for (; kb + 8 <= KB; kb += 8) {
       float pv[8], sv[8];
 #pragma unroll
       for (int x = 0; x < 8; ++x) {
-        pv[x] = pf[(kb + x) * kTok * kRows];
-        sv[x] = sf[(kb + x) * kSB * kTok];
+        pv[x] = pf[(kb + x) * kTokS * kRows];
+        sv[x] = sf[(kb + x) * kSB * kTokS];
       }
 #pragma unroll
       for (int x = 0; x < 8; ++x) acc = __builtin_fmaf(pv[x], sv[x], acc);
     }
-    for (; kb < KB; ++kb) acc = __builtin_fmaf(pf[kb * kTok * kRows], sf[kb * kSB * kTok], acc);
-    if (RAGGED || n0 + nl < N) out[(m_base + tok) * ldo + n0 + nl] = OutCvt<OutT>::cvt(acc);
+    for (; kb < KB; ++kb) acc = __builtin_fmaf(pf[kb * kTokS * kRows], sf[kb * kSB * kTokS], acc);
+    return acc;
+  };
+  const int live = RAGGED ? static_cast<int>(n_end - n0) : kRows;
+  for (int e = tid; e < live * kTok; e += kStreamWaves * 64) {
+    const int tok = e / live, nl = e - (e / live) * live;
+    if (tok >= m_rows) break;  // padding tokens: nothing to fold (later e only have larger tok)
+    const float* pf = part + tok * kRows + nl;
+    const float* sf = scl + (RAGGED && (n0 + nl) / kGroup != nb0 ? kTokS : 0) + tok;
+    if constexpr (SILU) {
+      // gate row n0 + nl and up row N / 2 + n0 + nl of this token, rounded to the GEMM's
+      // bf16 output, then silu = bf16(g / (1 + exp(-g))) and h = bf16(silu * u): the
+      // arithmetic of silu_mul_quant_kernel on the bf16 gate/up outputs.
+      const float* sfu = scl + (2 + ((n_rows + n0 + nl) / kGroup != nbu0 ? 1 : 0)) * kTokS + tok;
+      const float g = bf16_bits_val(OutCvt<bf16_t>::cvt(fold(pf, sf)));
+      const float u = bf16_bits_val(OutCvt<bf16_t>::cvt(fold(pf + 16 * kHalfT, sfu)));
+      const float silu = round_bf16(g / (1.0f + expf(-g)));
+      out[(m_base + tok) * ldo + n0 + nl] = f32_to_bf16_bits(silu * u);
+    } else {
+      const float acc = fold(pf, sf);
+      if (RAGGED || n0 + nl < N) out[(m_base + tok) * ldo + n0 + nl] = OutCvt<OutT>::cvt(acc);
+    }
   }
 }
 
@@ -720,10 +761,13 @@ int plan_gemm_on(int64_t M, int64_t N, int64_t K, int config, int64_t cus, GemmP
   if (config == MI355X_FP8_CONFIG_AUTO) {
     // Every kernel gives the same bits, so this is a speed choice only.  The stream kernel
     // re-reads the activations from L2 in every workgroup, so with more rows it keeps the
-    // lead only while the weight rows give few workgroups (measured on the Qwen3-4B
-    // shapes: at 64 rows o_proj / down 15 / 30 us streamed against 18 / 38 us tiled, qkv /
-    // gate_up 20 / 50 us against 13 / 22 us; at 32 rows gate_up 24 against 22 us).
-    const bool stream = M <= 16 || (M <= 64 && cdiv(N, 16) <= cus) || (M <= 32 && cdiv(N, 16) <= 2 * cus);
+    // lead only while the weight rows give few workgroups, and its re-reads grow with M x K.
+    // Measured on the Qwen3-4B shapes with the weights streamed from HBM (µs, streamed
+    // against tiled): o_proj (K = 4096) at 64 rows 10.8 / 12.9; down (K = 9728) at 48 rows
+    // 22.6 / 24.8, at 56 and 64 rows 27.4 / 25.6 and 29.8 / 26.3; qkv at 32 rows 9.1 / 9.5,
+    // at 40 rows 13.3 / 9.8; gate_up at 17 rows 19.4 / 16.1.
+    const bool stream = M <= 16 || (M <= 64 && cdiv(N, 16) <= cus && M * K <= 48 * 9728) ||
+                        (M <= 32 && cdiv(N, 16) <= 2 * cus);
     config = stream ? MI355X_FP8_CONFIG_STREAM : MI355X_FP8_CONFIG_TILE128;
   }
   if (config < MI355X_FP8_CONFIG_STREAM || config > MI355X_FP8_CONFIG_DMA64_128) return MI355X_FP8_ERR_INVALID;
@@ -1051,8 +1095,9 @@ static int launch_norm_linear_q(const GemmPlan& p, const bf16_t* x, int64_t sxm,
                                 uint16_t* out, int64_t ldo, int64_t M, int64_t N, int64_t K, hipStream_t stream) {
   const int64_t kb = cdiv(K, kGroup);
   const bool ragged = p.rows != 16 * AF || 8 % AF != 0;
-  // The fold buffer, the rows' 1 / rms, the norm weight and the M rows at pitch K + 8.
-  const size_t bytes = stream_fold_bytes(kb, AF, 1, ragged ? 2 : 1) + 16 * sizeof(float) +
+  // The fold buffer (8 token slots), the rows' 1 / rms, the norm weight and the M rows at
+  // pitch K + 8.
+  const size_t bytes = stream_fold_bytes(kb, AF, 1, ragged ? 2 : 1, 8) + 16 * sizeof(float) +
                        static_cast<size_t>(K + M * (K + 8)) * sizeof(uint16_t);
   // The rows staged in LDS take the buffer past the two-per-CU budget: one workgroup per CU
   // (a decode projection's stream grid holds about one per CU anyway) with all its LDS.
@@ -1111,6 +1156,72 @@ int launch_norm_linear(const GemmPlan& plan, const uint16_t* x, int64_t sxm, con
   if (M <= 2) return launch_norm_linear_af<2>(plan, xb, sxm, na, w, ldw, ws, ws_sn, ws_sk, out, ldo, M, N, K, stream);
   if (M <= 4) return launch_norm_linear_af<4>(plan, xb, sxm, na, w, ldw, ws, ws_sn, ws_sk, out, ldo, M, N, K, stream);
   return launch_norm_linear_af<8>(plan, xb, sxm, na, w, ldw, ws, ws_sn, ws_sk, out, ldo, M, N, K, stream);
+}
+
+// RMSNorm + gate/up GEMM + SiLU*up in one launch (stream_gemm_kernel with NORM and SILU):
+// `rows` gate rows and as many up rows per workgroup, AF / 2 MFMA tiles each.
+template <int AF, int QT>
+static int launch_norm_silu_q(int rows, const bf16_t* x, int64_t sxm, const NormArgs& na, const uint8_t* w,
+                              int64_t ldw, const float* ws, int64_t ws_sn, int64_t ws_sk, uint16_t* h, int64_t ldh,
+                              int64_t M, int64_t N, int64_t K, hipStream_t stream) {
+  const int64_t kb = cdiv(K, kGroup);
+  const size_t bytes = stream_fold_bytes(kb, AF, 1, 4, 8) + 16 * sizeof(float) +
+                       static_cast<size_t>(K + M * (K + 8)) * sizeof(uint16_t);
+  if (bytes > kNormLds) return MI355X_FP8_ERR_UNSUPPORTED;
+  const dim3 grid(static_cast<unsigned>(cdiv(N / 2, rows)), 1, 1);
+  stream_gemm_kernel<1, AF, true, true, bf16_t, bf16_t, QT, true, true><<<grid, kStreamWaves * 64, bytes, stream>>>(
+      reinterpret_cast<const uint8_t*>(x), sxm, nullptr, 0, 0, w, ldw, ws, ws_sn, ws_sk, h, ldh, M, N, K, kb, rows,
+      na);
+  return hipGetLastError() == hipSuccess ? MI355X_FP8_OK : MI355X_FP8_ERR_LAUNCH;
+}
+
+template <int QT>
+static int launch_norm_silu_af(int rows, const bf16_t* x, int64_t sxm, const NormArgs& na, const uint8_t* w,
+                               int64_t ldw, const float* ws, int64_t ws_sn, int64_t ws_sk, uint16_t* h, int64_t ldh,
+                               int64_t M, int64_t N, int64_t K, hipStream_t stream) {
+#define MI355X_NS_ARGS rows, x, sxm, na, w, ldw, ws, ws_sn, ws_sk, h, ldh, M, N, K, stream
+  switch (cdiv(rows, 16)) {
+    case 1: return launch_norm_silu_q<2, QT>(MI355X_NS_ARGS);
+    case 2: return launch_norm_silu_q<4, QT>(MI355X_NS_ARGS);
+    case 3: return launch_norm_silu_q<6, QT>(MI355X_NS_ARGS);
+    default: return MI355X_FP8_ERR_UNSUPPORTED;
+  }
+#undef MI355X_NS_ARGS
+}
+
+int launch_norm_gate_up_silu(const uint16_t* x, int64_t sxm, const uint16_t* res, int64_t ldr, uint16_t* res_out,
+                             int64_t ldro, const uint16_t* norm_w, float eps, const uint8_t* w, int64_t ldw,
+                             const float* ws, int64_t ws_sn, int64_t ws_sk, uint16_t* h, int64_t ldh, int64_t M,
+                             int64_t N, int64_t K, hipStream_t stream) {
+  // The one-launch norm-linear's conditions (launch_norm_linear), an even N whose halves start
+  // on a 16-byte row boundary, and h rows 4-byte aligned.
+  const auto a16 = [](const void* ptr) { return reinterpret_cast<uintptr_t>(ptr) % 16 == 0; };
+  if (M < 1 || M > 8 || N <= 0 || N % 2 != 0 || K % 256 != 0 || K / 256 > kNormMaxVec || sxm % 8 != 0 ||
+      ldw % 16 != 0 || !a16(x) || !a16(w) || !a16(norm_w) ||
+      (res != nullptr && (ldr % 8 != 0 || !a16(res) || res_out == nullptr || ldro % 8 != 0 || !a16(res_out))))
+    return MI355X_FP8_ERR_UNSUPPORTED;
+  const int bw = rmsnorm_block_width(M, K);
+  if (bw < 64 || bw > 512 || bw % 64 != 0) return MI355X_FP8_ERR_UNSUPPORTED;
+  // One workgroup per CU: the same number of gate rows (and up rows) on every CU, at least
+  // kStreamMinRows, at most three MFMA tiles of each.
+  const int64_t cus = device_cus();
+  const int64_t half = N / 2;
+  const int64_t rows = cdiv(half, cus) > kStreamMinRows ? cdiv(half, cus) : kStreamMinRows;
+  if (rows > 48 || cdiv(half, rows) > 0x7fffffffLL) return MI355X_FP8_ERR_UNSUPPORTED;
+  NormArgs na;
+  na.res = res;
+  na.ldr = ldr;
+  na.sum = res_out;
+  na.lds = ldro;
+  na.w = norm_w;
+  na.eps = eps;
+  na.inv_k = 1.0f / static_cast<float>(K);
+  na.bw = bw;
+  const bf16_t* xb = reinterpret_cast<const bf16_t*>(x);
+  const int r = static_cast<int>(rows);
+  if (M <= 2) return launch_norm_silu_af<2>(r, xb, sxm, na, w, ldw, ws, ws_sn, ws_sk, h, ldh, M, N, K, stream);
+  if (M <= 4) return launch_norm_silu_af<4>(r, xb, sxm, na, w, ldw, ws, ws_sn, ws_sk, h, ldh, M, N, K, stream);
+  return launch_norm_silu_af<8>(r, xb, sxm, na, w, ldw, ws, ws_sn, ws_sk, h, ldh, M, N, K, stream);
 }
 
 int launch_linear_stream(const GemmPlan& plan, const void* x, int x_dtype, int64_t sxm, int64_t sxk,

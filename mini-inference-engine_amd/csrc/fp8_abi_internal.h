@@ -58,6 +58,14 @@ int launch_norm_linear(const GemmPlan& plan, const uint16_t* x, int64_t sxm, con
                        int64_t ldw, const float* ws, int64_t ws_sn, int64_t ws_sk, uint16_t* out, int64_t ldo,
                        int64_t M, int64_t N, int64_t K, hipStream_t stream);
 
+// Residual add + RMSNorm + quantizer + merged gate/up GEMM + SiLU*up in one stream-kernel
+// launch: h[M, N / 2] = bf16(bf16(silu(gate)) * up); MI355X_FP8_ERR_UNSUPPORTED (nothing
+// launched) when the call does not fit that form.
+int launch_norm_gate_up_silu(const uint16_t* x, int64_t sxm, const uint16_t* res, int64_t ldr, uint16_t* res_out,
+                             int64_t ldro, const uint16_t* norm_w, float eps, const uint8_t* w, int64_t ldw,
+                             const float* ws, int64_t ws_sn, int64_t ws_sk, uint16_t* h, int64_t ldh, int64_t M,
+                             int64_t N, int64_t K, hipStream_t stream);
+
 // LDS-DMA pipelined prefill kernel (tile_gemm_dma.hip) and its preconditions.
 bool tile_dma_supported(const uint8_t* q, int64_t ldq, int64_t as_sm, int64_t as_sk, const uint8_t* w,
                         int64_t ldw, int64_t M, int64_t K);

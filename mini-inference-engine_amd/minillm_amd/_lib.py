@@ -52,6 +52,8 @@ EXPORTS = {
                                   _i64, _ptr, _i64, _i64, _ptr, _i64, _i64, _ptr], _int),
     "mi355x_fp8_rmsnorm_linear": ([_ptr, _i64, _i64, _i64, _ptr, _i64, _ptr, _i64, _ptr, ctypes.c_float, _ptr, _i64,
                                    _ptr, _i64, _i64, _i64, _ptr, _i64, _ptr], _int),
+    "mi355x_fp8_rmsnorm_gate_up_silu": ([_ptr, _i64, _i64, _i64, _ptr, _i64, _ptr, _i64, _ptr, ctypes.c_float, _ptr,
+                                         _i64, _ptr, _i64, _i64, _i64, _ptr, _i64, _ptr], _int),
     "mi355x_fp8_linear_workspace_bytes": ([_i64, _i64, _i64, _int], _size),
     "mi355x_fp8_linear_noalloc": ([_ptr, _int, _i64, _i64, _i64, _i64, _ptr, _i64, _ptr, _i64, _i64, _i64, _ptr,
                                    _int, _i64, _int, _ptr], _int),

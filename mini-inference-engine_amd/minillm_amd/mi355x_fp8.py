@@ -635,6 +635,56 @@ def rmsnorm_linear_mi355x_fp8(x: torch.Tensor, norm_weight: torch.Tensor, eps: f
     return (out, outs[2]) if residual is not None else out
 
 
+def rmsnorm_gate_up_silu_mi355x_fp8(x: torch.Tensor, norm_weight: torch.Tensor, eps: float,
+                                    gate_up_weight: torch.Tensor, gate_up_scale: torch.Tensor,
+                                    residual: torch.Tensor | None = None):
+    """``silu_mul(*project_gate_up(rms_norm(x [+ residual])))``: the post-attention norm, the
+    merged gate/up projection (weight rows: gate, then up) and SiLU(gate) * up, the input of
+    the down projection.  Returns h [..., I] (bf16), plus the residual sum when ``residual`` is
+    given.
+
+    Up to 8 rows (bf16, K a multiple of 256 up to 2560) the three run as one launch, each
+    workgroup owning matching gate and up weight rows; otherwise the norm-linear and the
+    SiLU*up kernel run separately.  Both give the same bits: h = bf16(bf16(silu(g)) * u) on the
+    projection's bf16 gate and up outputs, as ``silu_mul_quant_mi355x_fp8`` forms it."""
+
+    k = int(x.shape[-1])
+    n = int(gate_up_weight.shape[0])
+    inter = n // 2
+    x2 = x.reshape(-1, k)
+    if (x.dtype == torch.bfloat16 and norm_weight.dtype == torch.bfloat16 and x2.shape[0] <= 8 and n % 2 == 0
+            and x2.stride(-1) == 1 and gate_up_weight.dtype == torch.float8_e4m3fn and gate_up_weight.stride(-1) == 1
+            and gate_up_scale.dtype == torch.float32 and x.is_cuda and mi355x_available(x.device)
+            and gate_up_weight.device == x.device and gate_up_scale.device == x.device
+            and tuple(gate_up_scale.shape) == (-(-n // 128), -(-k // 128)) and tuple(norm_weight.shape) == (k,)
+            and (residual is None or (residual.shape == x.shape and residual.dtype == torch.bfloat16))):
+        m = int(x2.shape[0])
+        h = torch.empty((m, inter), device=x.device, dtype=torch.bfloat16)
+        r2 = summed = None
+        if residual is not None:
+            r2 = residual.reshape(-1, k)
+            if r2.stride(-1) != 1:
+                r2 = r2.contiguous()
+            summed = torch.empty((m, k), device=x.device, dtype=x.dtype)
+        w1 = norm_weight.contiguous()
+        code = _lib.load().mi355x_fp8_rmsnorm_gate_up_silu(
+            x2.data_ptr(), m, k, x2.stride(0), None if r2 is None else r2.data_ptr(), 0 if r2 is None else r2.stride(0),
+            None if summed is None else summed.data_ptr(), k, w1.data_ptr(), float(eps), gate_up_weight.data_ptr(),
+            gate_up_weight.stride(0), gate_up_scale.data_ptr(), gate_up_scale.stride(0), gate_up_scale.stride(1),
+            n, h.data_ptr(), h.stride(0), _stream_ptr(x.device))
+        if code != _lib.ERR_UNSUPPORTED:
+            _lib.check(code)
+            h = h.reshape(*x.shape[:-1], inter)
+            return (h, summed.reshape(x.shape)) if residual is not None else h
+
+    outs = rmsnorm_linear_mi355x_fp8(x, norm_weight, eps, gate_up_weight, gate_up_scale, residual)
+    gu = outs[0] if residual is not None else outs
+    gu2 = gu.reshape(-1, n)
+    h = silu_mul_quant_mi355x_fp8(gu2[:, :inter], gu2[:, inter:], return_intermediate=True)[0]
+    h = h.reshape(*x.shape[:-1], inter)
+    return (h, outs[1]) if residual is not None else h
+
+
 def mlp_forward_mi355x_fp8(x: torch.Tensor, gate_up_weight: torch.Tensor, gate_up_scale: torch.Tensor,
                            down_weight: torch.Tensor, down_scale: torch.Tensor,
                            output_dtype: torch.dtype | None = None) -> torch.Tensor:

@@ -368,3 +368,58 @@ def test_hip_graph_replays_match_eager(gpu):
         torch.cuda.synchronize()
         for got, want in zip(captured, eager):
             assert bitwise_equal(got, want), (replay, bit_mismatch_details(got, want))
+
+
+@pytest.mark.parametrize("shape", [ModelShape("gate_up", 19456, 2560), ModelShape("gate_up_small", 1024, 1024),
+                                   ModelShape("gate_up_ragged", 2 * 1408, 2560)], ids=lambda s: s.name)
+@pytest.mark.parametrize("rows", [1, 2, 3, 4, 5, 8, 9])
+@pytest.mark.parametrize("with_residual", [False, True])
+def test_rmsnorm_gate_up_silu_one_launch_equals_separate(gpu, shape, rows, with_residual):
+    """Up to 8 rows the post-attention norm, the merged gate/up GEMM and SiLU(gate) * up run as
+    one launch (each workgroup owning matching gate and up rows); h and the residual sum equal,
+    bit for bit, the norm-linear's gate_up output followed by the SiLU*up kernel's h.  The
+    widths cover the Qwen3-4B intermediate (three 16-row tiles per half, 38 rows per CU), a
+    narrow one (one tile) and one whose halves end inside a 128-row weight-scale block; 9 rows
+    take the separate launches.  h is also held to the oracle chain (rms_norm, linear,
+    silu_mul on its bf16 outputs)."""
+
+    _note("rmsnorm gate_up silu", shape.name, rows, with_residual)
+    gen = torch.Generator().manual_seed(rows * 13 + shape.n)
+    x = (torch.randn(rows, shape.k, generator=gen) * 2).to(torch.bfloat16)
+    x[0, :3] = torch.tensor([0.0, -0.0, 3000.0]).to(torch.bfloat16)
+    r = torch.randn(rows, shape.k, generator=gen).to(torch.bfloat16) if with_residual else None
+    nw = (torch.rand(shape.k, generator=gen) + 0.5).to(torch.bfloat16)
+    w, ws = make_weights(shape, 17)
+    xg, nwg, wg, wsg = x.to(gpu), nw.to(gpu), w.to(gpu), ws.to(gpu)
+    rg = None if r is None else r.to(gpu)
+    inter = shape.n // 2
+    got = fp8.rmsnorm_gate_up_silu_mi355x_fp8(xg, nwg, 1e-6, wg, wsg, residual=rg)
+    lin = fp8.rmsnorm_linear_mi355x_fp8(xg, nwg, 1e-6, wg, wsg, residual=rg)
+    gu = lin[0] if with_residual else lin
+    h_ref = fp8.silu_mul_quant_mi355x_fp8(gu[:, :inter], gu[:, inter:], return_intermediate=True)[0]
+    h = got[0] if with_residual else got
+    assert h.shape == (rows, inter) and h.dtype == torch.bfloat16
+    assert bitwise_equal(h, h_ref), bit_mismatch_details(h, h_ref)
+    if with_residual:
+        assert bitwise_equal(got[1], lin[1])
+    if rows <= 8:
+        # The one-launch entry point itself must take these shapes.
+        direct = torch.full((rows, inter), float("nan"), dtype=torch.bfloat16, device=gpu)
+        summed = torch.empty((rows, shape.k), dtype=torch.bfloat16, device=gpu) if with_residual else None
+        code = _lib.load().mi355x_fp8_rmsnorm_gate_up_silu(
+            xg.data_ptr(), rows, shape.k, xg.stride(0), None if rg is None else rg.data_ptr(),
+            0 if rg is None else rg.stride(0), None if summed is None else summed.data_ptr(), shape.k,
+            nwg.data_ptr(), 1e-6, wg.data_ptr(), wg.stride(0), wsg.data_ptr(), wsg.stride(0), wsg.stride(1),
+            shape.n, direct.data_ptr(), direct.stride(0), torch.cuda.current_stream(gpu).cuda_stream)
+        assert code == 0, f"one-launch entry point returned {code}"
+        torch.cuda.synchronize(gpu)
+        assert bitwise_equal(direct, h_ref), bit_mismatch_details(direct, h_ref)
+        if with_residual:
+            assert bitwise_equal(summed, lin[1])
+    # The oracle chain on the same stage inputs: the norm and the GEMM within the GEMM
+    # tolerance, SiLU*up on the GPU's own bf16 gate/up outputs within one bf16 ulp.
+    y_ref, _ = oracle.rmsnorm(bits16(xg), bits16(nwg), 1e-6, None if rg is None else bits16(rg))
+    gu_ref = _bf16(oracle.linear(y_ref, codes(w), ws.numpy()))
+    assert_close_rows(gu, gu_ref)
+    ulps = np.abs(bits16(h).astype(np.int32) - oracle.silu_mul(bits16(gu[:, :inter]), bits16(gu[:, inter:])).astype(np.int32))
+    assert ulps.max() <= 1
