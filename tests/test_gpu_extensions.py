@@ -371,7 +371,8 @@ def test_hip_graph_replays_match_eager(gpu):
 
 
 @pytest.mark.parametrize("shape", [ModelShape("gate_up", 19456, 2560), ModelShape("gate_up_small", 1024, 1024),
-                                   ModelShape("gate_up_ragged", 2 * 1408, 2560)], ids=lambda s: s.name)
+                                   ModelShape("gate_up_ragged", 2 * 1408, 2560), ModelShape("gate_up_odd", 2 * 259, 256),
+                                   ModelShape("gate_up_tiny", 2 * 16, 512)], ids=lambda s: s.name)
 @pytest.mark.parametrize("rows", [1, 2, 3, 4, 5, 8, 9])
 @pytest.mark.parametrize("with_residual", [False, True])
 def test_rmsnorm_gate_up_silu_one_launch_equals_separate(gpu, shape, rows, with_residual):
@@ -423,3 +424,25 @@ def test_rmsnorm_gate_up_silu_one_launch_equals_separate(gpu, shape, rows, with_
     assert_close_rows(gu, gu_ref)
     ulps = np.abs(bits16(h).astype(np.int32) - oracle.silu_mul(bits16(gu[:, :inter]), bits16(gu[:, inter:])).astype(np.int32))
     assert ulps.max() <= 1
+
+
+def test_rmsnorm_gate_up_silu_edge_cases(gpu):
+    """Zero rows give an empty h (and residual sum); an odd merged width is not a gate/up pair
+    and is refused by the one-launch entry point (status UNSUPPORTED, nothing launched)."""
+
+    k, n = 512, 2 * 64
+    nw = torch.ones(k, dtype=torch.bfloat16, device=gpu)
+    w, ws = make_weights(ModelShape("gu_edge", n, k), 3)
+    wg, wsg = w.to(gpu), ws.to(gpu)
+    empty = torch.empty((0, k), dtype=torch.bfloat16, device=gpu)
+    h, summed = fp8.rmsnorm_gate_up_silu_mi355x_fp8(empty, nw, 1e-6, wg, wsg, residual=empty)
+    assert h.shape == (0, n // 2) and summed.shape == (0, k)
+    x = torch.ones((2, k), dtype=torch.bfloat16, device=gpu)
+    w_odd, ws_odd = make_weights(ModelShape("gu_odd", n + 1, k), 3)
+    out = torch.full((2, n), 7.0, dtype=torch.bfloat16, device=gpu)
+    code = _lib.load().mi355x_fp8_rmsnorm_gate_up_silu(
+        x.data_ptr(), 2, k, k, None, 0, None, k, nw.data_ptr(), 1e-6, w_odd.to(gpu).data_ptr(), k,
+        ws_odd.to(gpu).data_ptr(), ws_odd.shape[1], 1, n + 1, out.data_ptr(), n, torch.cuda.current_stream(gpu).cuda_stream)
+    torch.cuda.synchronize(gpu)
+    assert code in (_lib.ERR_INVALID, _lib.ERR_UNSUPPORTED)
+    assert (out == 7.0).all().item()
