@@ -9,8 +9,10 @@ merged Qwen3-4B projections (qkv, o_proj, gate_up, down), on one GPU.
   before the timed region (the quantizer is timed separately, ``quant``) and all inputs are
   resident in HBM.  The GEMM reads K-group-major activation scales, the layout
   ``fp8_linear`` hands it.
-* Weights rotate through enough independent sets (> 512 MB) that no launch reads weights
-  still in the 256 MB MALL from the launch before.
+* Weights rotate so that no launch reads weights still in the 256 MB MALL: each projection
+  is timed over its own ring of weight buffers of more than 600 MiB (the 7 generated sets
+  plus copies of them at other addresses; qkv 40 buffers, o_proj 60, gate_up 13, down 26),
+  and the decode chain streams 7 whole layers (707 MB) per replay.
 * Timing: each projection's launches (one per weight set) are captured in a HIP graph and
   replayed K times between two HIP events recorded on the stream the kernels run on; the
   per-launch time is the elapsed time over K x sets launches, so ``roofline.achieved`` is
@@ -142,6 +144,16 @@ def main(argv=None) -> int:
     sets = max(2, -(-512 * 2**20 // layer_bytes) + 1)
     print(f"generating {sets} weight sets of {layer_bytes / 2**20:.1f} MiB", file=sys.stderr, flush=True)
     weights = [[make_baseline_weights(p, SEED + 1000 * s, device="cuda") for p in projs] for s in range(sets)]
+    # Per projection, a ring of weight buffers larger than the MALL: the generated sets, then
+    # copies of them (the same bytes at other addresses miss the caches just the same).
+    ring_bytes = 600 * 2**20
+    rings = []
+    for i, p in enumerate(projs):
+        ring = [weights[r][i] for r in range(sets)]
+        while len(ring) * p.n * p.k < ring_bytes:
+            w, ws = weights[len(ring) % sets][i]
+            ring.append((w.clone(), ws.clone()))
+        rings.append(ring)
 
     lib = fp8._lib.load()
     sink = torch.empty(8 * 1024, dtype=torch.int32, device=dev)
@@ -153,30 +165,31 @@ def main(argv=None) -> int:
             q, s = fp8.quantize_mi355x_fp8_activation(x, scale_layout="kgroup")
             out = torch.empty((m, p.n), dtype=torch.bfloat16, device=dev)
 
-            def gemms(i=i, q=q, s=s, out=out):
-                for r in range(sets):
-                    fp8.launch_block_gemm(q, weights[r][i][0], out, s, weights[r][i][1])
+            ring = rings[i]
+
+            def gemms(ring=ring, q=q, s=s, out=out):
+                for w, ws in ring:
+                    fp8.launch_block_gemm(q, w, out, s, ws)
 
             def quants(x=x):
                 for _ in range(sets):
                     fp8.quantize_mi355x_fp8_activation(x, scale_layout="kgroup")
 
-            def linears(i=i, x=x):
-                for r in range(sets):
-                    fp8.mi355x_fp8_linear(x, weights[r][i][0], weights[r][i][1], [128, 128])
+            def linears(ring=ring, x=x):
+                for w, ws in ring:
+                    fp8.mi355x_fp8_linear(x, w, ws, [128, 128])
 
-            def reads(i=i):
-                for r in range(sets):
-                    w8 = weights[r][i][0]
+            def reads(ring=ring):
+                for w8, _ in ring:
                     fp8._lib.check(lib.mi355x_fp8_read_probe(w8.data_ptr(), w8.numel(), sink.data_ptr(), sink.numel(),
                                                              torch.cuda.current_stream().cuda_stream))
 
-            per_launch.append(timed_graph(torch, stream, gemms, sets, args.steps, args.warmup, args.eager))
+            per_launch.append(timed_graph(torch, stream, gemms, len(ring), args.steps, args.warmup, args.eager))
             if probe:
-                probes.append(timed_graph(torch, stream, reads, sets, args.steps, args.warmup, args.eager))
+                probes.append(timed_graph(torch, stream, reads, len(ring), args.steps, args.warmup, args.eager))
             quant.append(timed_graph(torch, stream, quants, sets, args.steps, args.warmup, args.eager))
             if full_linear:
-                linear.append(timed_graph(torch, stream, linears, sets, args.steps, args.warmup, args.eager))
+                linear.append(timed_graph(torch, stream, linears, len(ring), args.steps, args.warmup, args.eager))
         return per_launch, quant, linear, probes
 
     results = {}
@@ -222,8 +235,9 @@ def main(argv=None) -> int:
         results["decode"]["layer_chain"] = bench_decode_layers(torch, fp8, stream, args, weights, projs)
     if not args.no_sweep:
         print("timing the M sweep", file=sys.stderr, flush=True)
-        results["sweep"] = bench_sweep(torch, fp8, stream, args, weights, projs)
-    del weights
+        results["sweep"] = bench_sweep(torch, fp8, stream, args, rings, projs)
+    ring_sizes = {p.name: len(r) for p, r in zip(projs, rings)}
+    del weights, rings
     torch.cuda.empty_cache()
 
     extras = {}
@@ -258,7 +272,8 @@ def main(argv=None) -> int:
                 "N(0,0.02) weights block-quantized to e4m3 with 128x128 fp32 scales",
         "config": {"workload": "Qwen3-4B merged projections qkv/o_proj/gate_up/down; prefill M=2048 "
                                "(value) and decode M=8 (decode.gbps); GEMM on pre-quantized activations",
-                   "prefill_m": pre["m"], "decode_m": dec["m"], "weight_sets": sets},
+                   "prefill_m": pre["m"], "decode_m": dec["m"], "weight_sets": sets,
+                   "weight_ring_buffers": ring_sizes},
         "decode": {"gbps": round(dec["gbps"], 1), "ms_per_step": round(dec["step_ms"], 4),
                    "frac_of_hbm": round(dec["gbps"] / PEAK_HBM_GBPS, 4),
                    "linear_gbps": round(dec["linear"]["gbps"], 1),
@@ -283,18 +298,17 @@ def main(argv=None) -> int:
     return 0
 
 
-def bench_sweep(torch, fp8, stream, args, weights, projs):
+def bench_sweep(torch, fp8, stream, args, rings, projs):
     """GEMM-only and whole-linear (quantizer included) rate of each projection over the
     reference's benchmark row counts (BENCH_MS, engine/kernels/sm89_fp8_validation.py:33),
     so the dispatch crossovers show: per M, per projection, µs, TFLOPS and GB/s (op-level
-    bytes), and the kernel the dispatch picked.  Weights rotate through the same sets as the
+    bytes), and the kernel the dispatch picked.  Weights rotate through the same rings as the
     headline phases; steps shrink with M so the sweep stays within a minute."""
 
     from minillm_amd.validation import gemm_bytes, linear_flops, make_baseline_activations
 
     lib = fp8._lib.load()
     cus = torch.cuda.get_device_properties(0).multi_processor_count
-    sets = len(weights)
     out = {}
     for m in (int(v) for v in args.sweep_ms.split(",") if v):
         steps = max(2, min(args.steps, (args.steps * 256) // max(m, 256)))
@@ -305,16 +319,18 @@ def bench_sweep(torch, fp8, stream, args, weights, projs):
             q, s = fp8.quantize_mi355x_fp8_activation(x, scale_layout="kgroup")
             o = torch.empty((m, p.n), dtype=torch.bfloat16, device="cuda")
 
-            def gemms(i=i, q=q, s=s, o=o):
-                for r in range(sets):
-                    fp8.launch_block_gemm(q, weights[r][i][0], o, s, weights[r][i][1])
+            ring = rings[i]
 
-            def linears(i=i, x=x):
-                for r in range(sets):
-                    fp8.mi355x_fp8_linear(x, weights[r][i][0], weights[r][i][1], [128, 128])
+            def gemms(ring=ring, q=q, s=s, o=o):
+                for w, ws in ring:
+                    fp8.launch_block_gemm(q, w, o, s, ws)
 
-            g_ms = timed_graph(torch, stream, gemms, sets, steps, 1, args.eager)
-            l_ms = timed_graph(torch, stream, linears, sets, steps, 1, args.eager)
+            def linears(ring=ring, x=x):
+                for w, ws in ring:
+                    fp8.mi355x_fp8_linear(x, w, ws, [128, 128])
+
+            g_ms = timed_graph(torch, stream, gemms, len(ring), steps, 1, args.eager)
+            l_ms = timed_graph(torch, stream, linears, len(ring), steps, 1, args.eager)
             flops, nbytes = linear_flops(m, p.n, p.k), gemm_bytes(m, p.n, p.k)
             kernel = fp8.dispatch_name(m, p.n, p.k, cus)
             row[p.name] = {"kernel": kernel, "gemm_us": round(g_ms * 1e3, 2), "linear_us": round(l_ms * 1e3, 2),
@@ -419,10 +435,21 @@ def bench_mlp(torch, fp8, stream, args, make_w, make_x):
     wgu, sgu = make_w(gu, SEED, device="cuda")
     wd, sd = make_w(down, SEED + 1, device="cuda")
     x = make_x(m, gu.k, SEED, outliers=True, device="cuda")
-    ms = timed_graph(torch, stream, lambda: fp8.mlp_forward_mi355x_fp8(x, wgu, sgu, wd, sd), 1, args.steps,
-                     args.warmup, args.eager)
+    # Copies of the block's 75 MB of weights at other addresses, more than 600 MiB in all, so
+    # that no call finds its weights in the MALL.
+    copies = [(wgu, sgu, wd, sd)]
+    while len(copies) * (gu.n * gu.k + down.n * down.k) < 600 * 2**20:
+        copies.append((wgu.clone(), sgu.clone(), wd.clone(), sd.clone()))
+
+    def blocks():
+        for a, b, c, d in copies:
+            fp8.mlp_forward_mi355x_fp8(x, a, b, c, d)
+
+    ms = timed_graph(torch, stream, blocks, len(copies), args.steps, args.warmup, args.eager)
     flops = 2 * m * (gu.n * gu.k + down.n * down.k)
-    return {"config": "MLP block M=512 (gate_up, fused SiLU*up + requant, down; incl. the input quantizer)",
+    del copies
+    return {"config": "MLP block M=512 (gate_up, fused SiLU*up + requant, down; incl. the input quantizer; "
+                      "weights rotated over > 600 MiB of copies)",
             "us": round(ms * 1e3, 2), "tflops": round(flops / (ms * 1e9), 1)}
 
 
