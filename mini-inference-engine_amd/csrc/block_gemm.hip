@@ -52,9 +52,10 @@ constexpr size_t kStreamFoldLds = 80 * 1024;
 constexpr size_t kStreamFoldLdsOne = 144 * 1024;
 constexpr int64_t kStreamMinRows = 8;
 
-// LDS of the one-round fold: the raw partials [KB][16 nt][16 af] and, per K group and token,
-// the scale products with the `blocks` (one, or two for ragged row counts) 128-row
-// weight-scale blocks a workgroup's rows touch.
+// LDS of the one-round fold: the raw partials [KB][tokens][16 af] and, per K group and token,
+// the scale products with the `blocks` (one, two for ragged row counts, four for the paired
+// gate/up rows) 128-row weight-scale blocks a workgroup's rows touch.  tokens = tok_slots when
+// given (the norm forms keep 8), else the slice's 16 nt.
 __host__ __device__ constexpr size_t stream_fold_bytes(int64_t kb, int af, int nt, int blocks = 1, int tok_slots = 0) {
   return static_cast<size_t>(kb) *
          (static_cast<size_t>(af) * 16 * (tok_slots ? tok_slots : 16 * nt) + blocks * (tok_slots ? tok_slots : 16 * nt)) *
